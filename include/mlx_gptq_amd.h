@@ -1,0 +1,149 @@
+/*
+ * mlx_gptq_amd.h -- C ABI of the MI355X-native GPTQ calibration solver.
+ *
+ * One shared library (libmlxgptq_hip.so, gfx950 code objects) replaces the
+ * torch/numpy arithmetic behind the reference's Python solver API
+ * (mlx_gptq/gptq.py, grid.py, packing.py, artifacts.py:30-39,
+ * capture.py:68-76). Each entry point below names the reference function it
+ * replaces as file:line, relative to the reference repository root.
+ *
+ * Conventions
+ *   - Plain C types only: device pointers, sizes, dtype/mode codes and a
+ *     hipStream_t passed as `void* stream` (0 = legacy default stream). All
+ *     work is enqueued on that stream; no call synchronises the device unless
+ *     its comment says so.
+ *   - Tensors are dense and row-major ("contiguous"); a [..., k] tensor is
+ *     passed as (pointer, n_groups = prod(leading dims), k).
+ *   - Return value: MGQ_OK (0) or a negative status. mgq_last_error() returns
+ *     the message of the calling thread's most recent failure. The Python
+ *     layer maps MGQ_ERR_VALUE -> ValueError, MGQ_ERR_SHAPE -> AssertionError,
+ *     MGQ_ERR_NOT_PD -> RuntimeError, as the reference raises them.
+ *   - Entry points are reentrant: they keep no mutable global state, so one
+ *     host thread per device may call them concurrently (the reference's
+ *     thread-per-device solve, sequential.py:610-626).
+ *   - Nothing here allocates device memory. Entry points that need scratch
+ *     take a caller-owned `workspace` of at least the size reported by the
+ *     matching *_workspace_size query.
+ */
+#ifndef MLX_GPTQ_AMD_H
+#define MLX_GPTQ_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define MGQ_OK 0
+#define MGQ_ERR_VALUE (-1)     /* unsupported mode / bits / algorithm          */
+#define MGQ_ERR_SHAPE (-2)     /* shape or divisibility violation              */
+#define MGQ_ERR_NOT_PD (-3)    /* Hessian not PD after damping escalation      */
+#define MGQ_ERR_HIP (-4)       /* HIP runtime / launch failure                 */
+#define MGQ_ERR_WORKSPACE (-5) /* workspace missing or too small               */
+
+/* ---- dtype / mode / method codes --------------------------------------- */
+#define MGQ_DTYPE_F32 0
+#define MGQ_DTYPE_BF16 1
+#define MGQ_DTYPE_F16 2
+
+#define MGQ_MODE_AFFINE 0
+#define MGQ_MODE_MXFP4 1
+#define MGQ_MODE_MXFP8 2
+
+#define MGQ_CLIP_MINMAX 0
+#define MGQ_CLIP_MSE 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mgq_version(void);
+
+/* Message of this thread's last failed call ("" if none). */
+const char* mgq_last_error(void);
+
+/* ======================================================================== *
+ * Quantization grids -- mlx_gptq/grid.py                                    *
+ * ======================================================================== */
+
+/* grid.py:61-79 choose_mxfp_scale(w, mode).
+ * w: f32 [n_groups, group_len] -> scale_bytes u8 [n_groups] (E8M0, e+127),
+ * scales f32 [n_groups] (= 2^e). mode: MGQ_MODE_MXFP4 (fmax 6) or _MXFP8
+ * (fmax 448). */
+int mgq_choose_mxfp_scale(const float* w, int64_t n_groups, int64_t group_len, int mode,
+                          uint8_t* scale_bytes, float* scales, void* stream);
+
+/* grid.py:108-124 quantize_mxfp_with_scale(w, scales, mode).
+ * w: f32 [n_groups, group_len], scales: f32 [n_groups] ->
+ * q u8 and dq f32, both [n_groups, group_len]. */
+int mgq_quantize_mxfp_with_scale(const float* w, const float* scales, int64_t n_groups,
+                                 int64_t group_len, int mode, uint8_t* q, float* dq,
+                                 void* stream);
+
+/* grid.py:127-139 dequantize_mxfp(q, scale_bytes, mode).
+ * q: u8 [n_groups, 32], scale_bytes: u8 [n_groups] -> out f32 [n_groups, 32]. */
+int mgq_dequantize_mxfp(const uint8_t* q, const uint8_t* scale_bytes, int64_t n_groups,
+                        int mode, float* out, void* stream);
+
+/* grid.py:142-151 rtn_quantize_mxfp(W, mode).
+ * W: [rows, cols] of w_dtype (f32/bf16/f16, read as f32), cols % 32 == 0 ->
+ * q u8 [rows, cols], scale_bytes u8 [rows, cols/32], dq f32 [rows, cols]. */
+int mgq_rtn_quantize_mxfp(const void* W, int w_dtype, int64_t rows, int64_t cols, int mode,
+                          uint8_t* q, uint8_t* scale_bytes, float* dq, void* stream);
+
+/* grid.py:154-164 dequantize_artifact, affine branch: q*scale + bias.
+ * q: u8 [n_groups, group_size]; scales, biases: storage_dtype [n_groups]. */
+int mgq_dequantize_affine(const uint8_t* q, const void* scales, const void* biases,
+                          int storage_dtype, int64_t n_groups, int64_t group_size, float* out,
+                          void* stream);
+
+/* grid.py:167-212 choose_qparams(w, bits, method, storage_dtype, grid_steps,
+ * max_shrink). w: f32 [n_groups, group_len] -> s_store, b_store in
+ * storage_dtype and s32, b32 f32, all [n_groups]. method: MGQ_CLIP_*. */
+int mgq_choose_qparams(const float* w, int64_t n_groups, int64_t group_len, int bits,
+                       int method, int storage_dtype, int grid_steps, double max_shrink,
+                       void* s_store, void* b_store, float* s32, float* b32, void* stream);
+
+/* grid.py:215-221 quantize_with_params(w, s32, b32, bits).
+ * w: f32 [n_groups, group_len]; s32, b32: f32 [n_groups] -> q f32, dq f32. */
+int mgq_quantize_with_params(const float* w, const float* s32, const float* b32,
+                             int64_t n_groups, int64_t group_len, int bits, float* q, float* dq,
+                             void* stream);
+
+/* grid.py:224-246 rtn_quantize(W, bits, group_size, method, storage_dtype).
+ * W: [rows, cols] of w_dtype -> q u8 [rows, cols], s_store/b_store
+ * storage_dtype [rows, cols/group_size], dq f32 [rows, cols]. Uses the
+ * reference's default grid (20 steps, max_shrink 0.2). */
+int mgq_rtn_quantize_affine(const void* W, int w_dtype, int64_t rows, int64_t cols, int bits,
+                            int group_size, int method, int storage_dtype, uint8_t* q,
+                            void* s_store, void* b_store, float* dq, void* stream);
+
+/* ======================================================================== *
+ * Packing -- mlx_gptq/packing.py, mlx_gptq/artifacts.py                     *
+ * ======================================================================== */
+
+/* packing.py:15-26 pack_q(q, bits): u8 [rows, cols] -> u32 [rows, cols*bits/32],
+ * LSB-first, codes not masked (as the numpy original). bits in {2, 4, 8};
+ * cols % (32/bits) == 0. pack_mxfp4 (packing.py:29-31) is bits = 4. */
+int mgq_pack_q(const uint8_t* q, int64_t rows, int64_t cols, int bits, uint32_t* words,
+               void* stream);
+
+/* packing.py:34-39 unpack_q(words, bits, out_cols): u32 [rows, n_words] ->
+ * u8 [rows, out_cols], out_cols <= n_words*32/bits. */
+int mgq_unpack_q(const uint32_t* words, int64_t rows, int64_t n_words, int bits,
+                 int64_t out_cols, uint8_t* q, void* stream);
+
+/* artifacts.py:30-32 pack_nibbles(q): u8 [rows, cols] -> u8 [rows, cols/2],
+ * byte = q[2k] | (q[2k+1] << 4) in uint8 arithmetic; cols even. */
+int mgq_pack_nibbles(const uint8_t* q, int64_t rows, int64_t cols, uint8_t* packed,
+                     void* stream);
+
+/* artifacts.py:35-39 unpack_nibbles(p): u8 [rows, packed_cols] ->
+ * u8 [rows, 2*packed_cols] (low nibble first). */
+int mgq_unpack_nibbles(const uint8_t* packed, int64_t rows, int64_t packed_cols, uint8_t* q,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLX_GPTQ_AMD_H */
