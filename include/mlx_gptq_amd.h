@@ -142,6 +142,38 @@ int mgq_pack_nibbles(const uint8_t* q, int64_t rows, int64_t cols, uint8_t* pack
 int mgq_unpack_nibbles(const uint8_t* packed, int64_t rows, int64_t packed_cols, uint8_t* q,
                        void* stream);
 
+/* ======================================================================== *
+ * Hessian accumulation -- mlx_gptq/capture.py:68-76 (Stash.hessian)        *
+ * ======================================================================== */
+
+/* Plan a grouped Hessian launch (host only, no device work).
+ * Group g owns entries [offsets[g], offsets[g+1]) of the token list
+ * (offsets: host int64 [n_groups+1], non-decreasing). target_items <= 0
+ * picks a default grid size. With plan == NULL only the sizes are returned:
+ * plan_bytes (host plan size) and workspace_bytes (device workspace size,
+ * which includes the plan). Otherwise the plan is written to `plan`
+ * (plan_capacity bytes available). */
+int mgq_hessian_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t target_items,
+                     void* plan, int64_t plan_capacity, int64_t* plan_bytes,
+                     int64_t* workspace_bytes);
+
+/* capture.py:68-76 Stash.hessian for every group at once:
+ *   H[g] (+)= X_g^T X_g,  X_g = rows row_index[offsets[g] .. offsets[g+1])
+ * of X (row_index == NULL: rows offsets[g] .. offsets[g+1] themselves).
+ * X: bf16 [n_rows, ldx] (device, 16-byte aligned; C and ldx multiples of 8;
+ * C <= 46340), row_index entries must lie in [0, n_rows) (out-of-range
+ * entries are clamped, never dereferenced) and the list must hold at least
+ * offsets[n_groups] entries,
+ * row_index: int32 device array or NULL, H: f32 [n_groups, C, C] device.
+ * accumulate = 0 overwrites H, 1 adds into it. H comes out exactly
+ * symmetric. plan_host: the plan from mgq_hessian_plan; the caller must have
+ * copied it (plan_bytes) to the start of `workspace` before this call, in
+ * stream order. bf16 x bf16 products are exact in fp32 and accumulated by
+ * v_mfma_f32_32x32x16_bf16. */
+int mgq_hessian(const void* X, int64_t n_rows, int64_t ldx, int64_t C,
+                const int32_t* row_index, const void* plan_host, float* H, int accumulate, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

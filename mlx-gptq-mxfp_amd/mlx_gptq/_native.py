@@ -61,6 +61,9 @@ SIGNATURES: dict[str, list] = {
     "mgq_unpack_q": [_VP, _I64, _I64, _INT, _I64, _VP, _VP],
     "mgq_pack_nibbles": [_VP, _I64, _I64, _VP, _VP],
     "mgq_unpack_nibbles": [_VP, _I64, _I64, _VP, _VP],
+    # capture.py Hessians
+    "mgq_hessian_plan": [_I64, _I64, _VP, _I64, _VP, _I64, _VP, _VP],
+    "mgq_hessian": [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _INT, _VP, _I64, _VP],
 }
 
 _RESTYPES = {"mgq_last_error": ctypes.c_char_p}
