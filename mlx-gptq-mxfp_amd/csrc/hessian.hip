@@ -39,6 +39,9 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+// Native clang vectors (not HIP's u32x4 struct) so register arrays of them
+// are promoted to VGPRs instead of private memory.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;
 constexpr int kKs = 64;          // tokens per LDS stage
@@ -83,50 +86,63 @@ __device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) 
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
-// Load the thread's 8 (tokens) x 8 (channels) bf16 blocks of the A and (off
-// the diagonal) B tiles: one 16-byte load per token and operand. Loads are
-// unconditional (out-of-range tokens/channels read a clamped valid address)
-// and zeroed afterwards, so the loop has no divergent branches.
+// Per-stage global traffic of a loader thread: its 8 tokens' rows (one
+// 16-byte load per token and operand). The three steps are kept apart so the
+// loop can software-pipeline them: gather indices for stage s+2 and row
+// loads for stage s+1 are in flight while stage s runs on the MFMAs; the
+// zero-masking of out-of-range tokens happens only when the rows are stored
+// to LDS. Everything is branch-free (a branch around a load makes the
+// compiler wait for it at the join). Out-of-range tokens read a clamped
+// valid row; gathered indices are clamped into X so a bad index cannot
+// fault.
 template <bool GATHER>
-__device__ inline void load_blocks(const uint16_t* __restrict__ X, int64_t ldx, int64_t n_rows,
-                                   const int32_t* __restrict__ row_index, int64_t tok0,
-                                   int64_t t_end, int64_t chanA, int64_t chanB, bool okA,
-                                   bool okB, bool diag, uint4 (&ra)[8], uint4 (&rb)[8]) {
+__device__ inline void load_index(const int32_t* __restrict__ row_index, int64_t tok0,
+                                  int64_t t_end, int32_t (&idx)[8]) {
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int64_t t = tok0 + r;
-    const bool tok_ok = t < t_end;
-    const int64_t tc = tok_ok ? t : t_end - 1;
-    // gathered rows are clamped into X so a bad index cannot fault
-    const int64_t row =
-        GATHER ? min(max(static_cast<int64_t>(row_index[tc]), int64_t(0)), n_rows - 1) : tc;
-    const uint16_t* p = X + row * ldx;
-    const uint4 va = *reinterpret_cast<const uint4*>(p + chanA);
-    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-    ra[r] = (tok_ok && okA) ? va : z;
-    if (!diag) {
-      const uint4 vb = *reinterpret_cast<const uint4*>(p + chanB);
-      rb[r] = (tok_ok && okB) ? vb : z;
-    }
+    idx[r] = GATHER ? row_index[t < t_end ? t : t_end - 1] : 0;
   }
+}
+
+template <bool GATHER>
+__device__ inline void load_rows(const uint16_t* __restrict__ X, int64_t ldx, int64_t n_rows,
+                                 const int32_t (&idx)[8], int64_t tok0, int64_t t_end,
+                                 int64_t chanA, int64_t chanB, u32x4 (&ra)[8], u32x4 (&rb)[8]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t t = tok0 + r;
+    const int64_t row = GATHER ? min(max(static_cast<int64_t>(idx[r]), int64_t(0)), n_rows - 1)
+                               : (t < t_end ? t : t_end - 1);
+    const uint16_t* p = X + row * ldx;
+    ra[r] = *reinterpret_cast<const u32x4*>(p + chanA);
+    rb[r] = *reinterpret_cast<const u32x4*>(p + chanB);
+  }
+}
+
+__device__ inline void mask_rows(int64_t tok0, int64_t t_end, bool ok, u32x4 (&rr)[8]) {
+  const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rr[r] = (ok && tok0 + r < t_end) ? rr[r] : z;
 }
 
 // Transpose an 8x8 bf16 block in registers (v_perm) so each channel's 8
 // tokens are contiguous, and store the 8 channel rows into the swizzled LDS
 // tile. Row cb*8+c, chunk kb lands at (cb*8+c)*8 + (kb ^ f(row)) with
 // f(row) = (c ^ cb) & 7, i.e. chunk (u ^ c) for u = (kb ^ cb) & 7.
-__device__ inline void store_block(uint4* __restrict__ lds, int cb, int u, const uint4 (&in)[8]) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(in);  // w[r*4 + d]
-  uint4* base = lds + cb * 64;
+__device__ inline uint32_t dword(const u32x4& v, int d) { return v[d]; }
+
+__device__ inline void store_block(u32x4* __restrict__ lds, int cb, int u, const u32x4 (&in)[8]) {
+  u32x4* base = lds + cb * 64;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-    const int d = c >> 1;
-    uint4 o;
-    o.x = perm(w[1 * 4 + d], w[0 * 4 + d], sel);
-    o.y = perm(w[3 * 4 + d], w[2 * 4 + d], sel);
-    o.z = perm(w[5 * 4 + d], w[4 * 4 + d], sel);
-    o.w = perm(w[7 * 4 + d], w[6 * 4 + d], sel);
+    const int d = c >> 1;  // dword holding channel c of each token
+    u32x4 o;
+    o.x = perm(dword(in[1], d), dword(in[0], d), sel);
+    o.y = perm(dword(in[3], d), dword(in[2], d), sel);
+    o.z = perm(dword(in[5], d), dword(in[4], d), sel);
+    o.w = perm(dword(in[7], d), dword(in[6], d), sel);
     base[c * 8 + (u ^ c)] = o;
   }
 }
@@ -175,7 +191,7 @@ __global__ void __launch_bounds__(kThreads, 1)
     syrk_tile_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
                      const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
                      float* __restrict__ H, float* __restrict__ partials, int accumulate) {
-  __shared__ uint4 lds[2][2][kTile * 8];  // 2 bufs x (A, B) x 256 rows x 128 B = 128 KB
+  __shared__ u32x4 lds[2][2][kTile * 8];  // 2 bufs x (A, B) x 256 rows x 128 B = 128 KB
 
   const HessItem it = items[blockIdx.x];
   if (it.g < 0) return;
@@ -197,9 +213,10 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int64_t cA = static_cast<int64_t>(it.ti) * kTile + cb * 8;
   const int64_t cB = static_cast<int64_t>(it.tj) * kTile + cb * 8;
   const bool okA = cA < C, okB = cB < C;
-  const int64_t chanA = okA ? cA : 0, chanB = okB ? cB : 0;
+  const int64_t chanA = okA ? cA : 0;
+  const int64_t chanB = diag ? chanA : (okB ? cB : 0);
 
-  // MFMA operand offsets (uint4 units) within a 256-row LDS tile: row
+  // MFMA operand offsets (u32x4 units) within a 256-row LDS tile: row
   // base + 32m + l, chunk 2ks + h lands at row*8 + ((2ks + h) ^ f(row)) with
   // f(row) = (l ^ (l >> 3) ^ 4(m & 1)) & 7, so only xo[ks ^ 2(m & 1)] varies.
   const int l = lane & 31, h = lane >> 5;
@@ -217,11 +234,17 @@ __global__ void __launch_bounds__(kThreads, 1)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[ma][na][r] = 0.0f;
 
-  uint4 ra[8], rb[8];
+  u32x4 ra[8], rb[8];
+  int32_t idx[8];
   const int64_t k0 = it.k0, k1 = it.k1;
   const int n_stages = static_cast<int>((k1 - k0 + kKs - 1) / kKs);
+  const int64_t tk = k0 + kb * 8;  // this thread's first token of stage 0
   if (n_stages > 0) {
-    load_blocks<GATHER>(X, ldx, n_rows, row_index, k0 + kb * 8, k1, chanA, chanB, okA, okB, diag, ra, rb);
+    load_index<GATHER>(row_index, tk, k1, idx);
+    load_rows<GATHER>(X, ldx, n_rows, idx, tk, k1, chanA, chanB, ra, rb);
+    if (n_stages > 1) load_index<GATHER>(row_index, tk + kKs, k1, idx);
+    mask_rows(tk, k1, okA, ra);
+    mask_rows(tk, k1, okB, rb);
     store_block(lds[0][0], cb, u, ra);
     if (!diag) store_block(lds[0][1], cb, u, rb);
   }
@@ -229,12 +252,13 @@ __global__ void __launch_bounds__(kThreads, 1)
   for (int s = 0; s < n_stages; ++s) {
     const int buf = s & 1;
     const bool more = s + 1 < n_stages;
+    const int64_t t1 = tk + static_cast<int64_t>(s + 1) * kKs;  // stage s+1
     if (more) {
-      const int64_t t0 = k0 + static_cast<int64_t>(s + 1) * kKs + kb * 8;
-      load_blocks<GATHER>(X, ldx, n_rows, row_index, t0, k1, chanA, chanB, okA, okB, diag, ra, rb);
+      load_rows<GATHER>(X, ldx, n_rows, idx, t1, k1, chanA, chanB, ra, rb);
+      if (s + 2 < n_stages) load_index<GATHER>(row_index, t1 + kKs, k1, idx);
     }
-    const uint4* A = lds[buf][0] + a_base;
-    const uint4* B = (diag ? lds[buf][0] : lds[buf][1]) + b_base;
+    const u32x4* A = lds[buf][0] + a_base;
+    const u32x4* B = (diag ? lds[buf][0] : lds[buf][1]) + b_base;
 #pragma unroll
     for (int ks = 0; ks < kKs / 16; ++ks) {
       bf16x8_t af[4], bfv[4];
@@ -252,6 +276,8 @@ __global__ void __launch_bounds__(kThreads, 1)
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ma], bfv[na], acc[ma][na], 0, 0, 0);
     }
     if (more) {
+      mask_rows(t1, k1, okA, ra);
+      mask_rows(t1, k1, okB, rb);
       store_block(lds[buf ^ 1][0], cb, u, ra);
       if (!diag) store_block(lds[buf ^ 1][1], cb, u, rb);
     }
@@ -316,35 +342,55 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
   chunk = std::min<int64_t>(chunk, kMaxItemTokens);
   chunk = ceil_div(chunk, kKs) * kKs;
 
-  // groups sorted by load, spread over XCDs (LPT)
-  std::vector<int64_t> order(n_groups);
-  std::iota(order.begin(), order.end(), 0);
-  std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
-    return (offsets[a + 1] - offsets[a]) > (offsets[b + 1] - offsets[b]);
-  });
-  std::vector<std::vector<HessItem>> bins(kXcds);
-  std::vector<int64_t> load(kXcds, 0);
+  // Work units: a group's items (tiles x K splits) in tile order, cut into at
+  // most 8 contiguous chunks of >= 32 items (one XCD has 32 CUs). Small groups
+  // (one expert) stay whole on one XCD so their token rows are reused from
+  // that XCD's L2; big dense groups spread over all XCDs. Chunks go to the
+  // least-loaded XCD, heaviest first (LPT).
+  struct Chunk {
+    int64_t work;
+    std::vector<HessItem> items;
+  };
+  std::vector<Chunk> chunks;
   int64_t n_slots = 0;
-  for (int64_t g : order) {
+  for (int64_t g = 0; g < n_groups; ++g) {
     const int64_t k0 = offsets[g], k1 = offsets[g + 1];
     const int64_t n = k1 - k0;
     const int64_t S = std::max<int64_t>(1, ceil_div(n, chunk));
-    const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
-    load[x] += std::max<int64_t>(n, 1) * T;
+    const int64_t per = ceil_div(ceil_div(std::max<int64_t>(n, 1), S), kKs) * kKs;
+    std::vector<HessItem> gi;
     for (const auto& t : tiles) {
       if (S == 1) {
-        bins[x].push_back(HessItem{static_cast<int32_t>(g), t.first, t.second, -1, k0, k1});
+        gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second, -1, k0, k1});
       } else {
-        const int64_t per = ceil_div(ceil_div(n, S), kKs) * kKs;
         const int32_t slot0 = static_cast<int32_t>(n_slots);
         int32_t ns = 0;
         for (int64_t a = k0; a < k1; a += per, ++ns) {
-          bins[x].push_back(HessItem{static_cast<int32_t>(g), t.first, t.second,
-                                     static_cast<int32_t>(n_slots++), a, std::min(a + per, k1)});
+          gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second,
+                                static_cast<int32_t>(n_slots++), a, std::min(a + per, k1)});
         }
         plan->split.push_back(SplitTile{static_cast<int32_t>(g), t.first, t.second, slot0, ns, 0});
       }
     }
+    const int64_t n_items = static_cast<int64_t>(gi.size());
+    const int64_t parts = std::min<int64_t>(kXcds, std::max<int64_t>(1, n_items / 32));
+    const int64_t step = ceil_div(n_items, parts);
+    for (int64_t a = 0; a < n_items; a += step) {
+      Chunk c;
+      c.items.assign(gi.begin() + a, gi.begin() + std::min(a + step, n_items));
+      c.work = 0;
+      for (const auto& it : c.items) c.work += std::max<int64_t>(it.k1 - it.k0, 1);
+      chunks.push_back(std::move(c));
+    }
+  }
+  std::stable_sort(chunks.begin(), chunks.end(),
+                   [](const Chunk& a, const Chunk& b) { return a.work > b.work; });
+  std::vector<std::vector<HessItem>> bins(kXcds);
+  std::vector<int64_t> load(kXcds, 0);
+  for (auto& c : chunks) {
+    const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    load[x] += c.work;
+    bins[x].insert(bins[x].end(), c.items.begin(), c.items.end());
   }
   size_t longest = 0;
   for (auto& b : bins) longest = std::max(longest, b.size());
