@@ -174,6 +174,44 @@ int mgq_hessian(const void* X, int64_t n_rows, int64_t ldx, int64_t C,
                 const int32_t* row_index, const void* plan_host, float* H, int accumulate, void* workspace,
                 int64_t workspace_bytes, void* stream);
 
+/* ======================================================================== *
+ * Solver -- mlx_gptq/gptq.py                                                *
+ * ======================================================================== */
+
+/* gptq.py:27-66 _prepare_hinv for every 32x32 diagonal block:
+ * U[b, g] (upper, f32 [B, C/32, 32, 32]) with U^T U = (Hb + lam I)^-1,
+ * lam = damp * max(mean(diag Hb), 1e-8), damp escalated x10 per block up to
+ * max_attempts times. attempts[g*B + b] = attempts used (1..max_attempts),
+ * or 0 when every attempt failed (the reference's RuntimeError case; U is
+ * zero there). H: f32 [B, C, C], C % 32 == 0; block must be 32. */
+int mgq_prepare_hinv_blocks(const float* H, int64_t B, int64_t C, int64_t block, float damp,
+                            int max_attempts, float* U, int32_t* attempts, void* stream);
+
+/* Workspace bytes needed by mgq_gptq_mxfp for W [B, R, C]. */
+int64_t mgq_gptq_mxfp_workspace_size(int64_t B, int64_t R, int64_t C);
+
+/* gptq.py:183-272 gptq_quantize / 275-302 solve_gptq for mode mxfp4 / mxfp8
+ * (gptq.py:69-180 _gptq_quantize_mxfp_groupwise), one launch sequence:
+ *   dead-column fix (gptq.py:216-222: diag(H) <= 0 -> diagonal set to 1 in
+ *   place in H, weights of that column treated as 0), per-group damped
+ *   Cholesky-inverse (mgq_prepare_hinv_blocks), fused group solver.
+ * W: [B, R, C] of w_dtype (f32 / bf16 / f16), H: f32 [B, C, C] (modified in
+ * place as the reference does), C % 32 == 0.
+ * mode: MGQ_MODE_MXFP4 / MGQ_MODE_MXFP8. algorithm: 0 = groupwise,
+ * 1 = safe-scale-search with exponent `offsets[n_offsets]` tried in order
+ * (reference: {0,-1,-2,-3,-4,1,2} for mxfp4, {0,-1,1} for mxfp8; <= 8).
+ * Outputs: q_out u8 [B, R, C], scales_out u8 [B, R, C/32] (E8M0),
+ * W_dq f32 [B, R, C] (may alias W when w_dtype is f32), rel_err f32 [B]
+ * (||W_dq - W||_F / max(||W||_F, 1e-12), NULL to skip), attempts i32
+ * [C/32, B] (see mgq_prepare_hinv_blocks; any 0 means the reference would
+ * raise its "not positive definite" RuntimeError -- outputs are then
+ * unspecified). workspace: mgq_gptq_mxfp_workspace_size bytes. */
+int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, float* H,
+                  int mode, int algorithm, float damp, int max_attempts, const int32_t* offsets,
+                  int n_offsets, uint8_t* q_out, uint8_t* scales_out, float* W_dq,
+                  float* rel_err, int32_t* attempts, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

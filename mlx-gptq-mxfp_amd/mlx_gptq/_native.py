@@ -64,9 +64,14 @@ SIGNATURES: dict[str, list] = {
     # capture.py Hessians
     "mgq_hessian_plan": [_I64, _I64, _VP, _I64, _VP, _I64, _VP, _VP],
     "mgq_hessian": [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _INT, _VP, _I64, _VP],
+    # gptq.py solver
+    "mgq_prepare_hinv_blocks": [_VP, _I64, _I64, _I64, _F32, _INT, _VP, _VP, _VP],
+    "mgq_gptq_mxfp_workspace_size": [_I64, _I64, _I64],
+    "mgq_gptq_mxfp": [_VP, _INT, _I64, _I64, _I64, _VP, _INT, _INT, _F32, _INT, _VP, _INT,
+                      _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
 }
 
-_RESTYPES = {"mgq_last_error": ctypes.c_char_p}
+_RESTYPES = {"mgq_last_error": ctypes.c_char_p, "mgq_gptq_mxfp_workspace_size": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()

@@ -1,0 +1,217 @@
+"""Batched GPTQ solver on MI355X behind the reference solver API.
+
+Same entry points, arguments, defaults, return tuples, in-place semantics,
+warnings and exceptions as the reference module mlx_gptq/gptq.py:
+
+  _prepare_hinv(H, damp, max_attempts=6)                      gptq.py:27-66
+  _gptq_quantize_mxfp_groupwise(W, H, mode, damp, algorithm)  gptq.py:69-180
+  gptq_quantize(W, H, bits, group_size, ...)                  gptq.py:183-272
+  solve_gptq(W_orig, H, bits, group_size, ...)                gptq.py:275-302
+
+W is [B, out, in] (B = batched experts, 1 for a dense linear), H is
+[B, in, in]. The arithmetic runs in the HIP kernels of libmlxgptq_hip.so
+(csrc/cholesky.hip, csrc/gptq_mxfp.hip, csrc/gptq_affine.hip); this module
+validates arguments, allocates outputs/workspace with torch on the tensors'
+device, reproduces the reference's damping-escalation warnings from the
+per-block attempt counts the kernels report, and raises its RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .grid import MX_GROUP_SIZE
+
+log = logging.getLogger(__name__)
+
+MXFP4_OFFSETS = (0, -1, -2, -3, -4, 1, 2)
+MXFP8_OFFSETS = (0, -1, 1)
+
+
+def _escalation_report(attempts: np.ndarray, B: int, damp: float, max_attempts: int,
+                       H_blocks) -> None:
+    """Emit the reference's per-round warnings for one _prepare_hinv call and
+    raise its RuntimeError if some block never factorised (gptq.py:37-63).
+
+    attempts: int [B] (attempts used, 0 = failed every attempt).
+    H_blocks: callable(failed_index_array) -> float tensor [F, n, n] of the
+    undamped blocks, used only for the failure message.
+    """
+    failed_all = attempts == 0
+    rounds = max_attempts if failed_all.any() else int(attempts.max()) - 1
+    cur = np.float32(damp)
+    for r in range(max(rounds, 0)):
+        cur = np.float32(cur * np.float32(10.0))
+        failed = failed_all | (attempts > r + 1)
+        log.warning("cholesky failed for %d/%d matrices, damp -> %.3g", int(failed.sum()), B, float(cur))
+    if failed_all.any():
+        bad = H_blocks(np.nonzero(failed_all)[0])
+        diag = bad.diagonal(dim1=-2, dim2=-1)
+        raise RuntimeError(
+            "Hessian not positive definite after damping escalation; "
+            f"batch={B} failed={int(failed_all.sum())} "
+            f"nonfinite={int((~torch.isfinite(bad)).sum())} "
+            f"diag_min={float(diag.min())} diag_max={float(diag.max())} "
+            f"value_min={float(bad.min())} value_max={float(bad.max())}"
+        )
+
+
+def _prepare_hinv(H: torch.Tensor, damp: float, max_attempts: int = 6) -> torch.Tensor:
+    """Upper Cholesky factor of (H + damp*mean(diag)*I)^-1, batched, with
+    per-item damping escalation (gptq.py:27-66). H: float32 [B, C, C]."""
+    B, C, _ = H.shape
+    dev = nat.device_for(H)
+    Hc = nat.on_device(H.float(), dev)
+    if C == MX_GROUP_SIZE:
+        U = torch.empty(B, C, C, dtype=torch.float32, device=dev)
+        att = torch.empty(B, dtype=torch.int32, device=dev)
+        nat.call("mgq_prepare_hinv_blocks", Hc.data_ptr(), B, C, C, float(damp),
+                 int(max_attempts), U.data_ptr(), att.data_ptr(), nat.stream_of(dev))
+    else:
+        from . import gptq_affine
+
+        U, att = gptq_affine.prepare_hinv_full(Hc, damp, max_attempts)
+    _escalation_report(att.cpu().numpy(), B, damp, max_attempts, lambda idx: Hc[torch.as_tensor(idx, device=dev)])
+    return U.to(H.device)
+
+
+def _mxfp_solve(W_in: torch.Tensor, H: torch.Tensor, mode: str, damp: float, algorithm: str,
+                W_out: torch.Tensor, want_rel: bool):
+    """Launch the fused MXFP solver; returns (q, scales, rel|None)."""
+    if algorithm not in ("groupwise", "safe-scale-search"):
+        raise ValueError(f"unsupported MXFP GPTQ algorithm: {algorithm}")
+    B, R, C = W_in.shape
+    dev = W_out.device
+    q = torch.empty(B, R, C, dtype=torch.uint8, device=dev)
+    scales = torch.empty(B, R, C // MX_GROUP_SIZE, dtype=torch.uint8, device=dev)
+    rel = torch.empty(B, dtype=torch.float32, device=dev) if want_rel else None
+    att = torch.empty(C // MX_GROUP_SIZE, B, dtype=torch.int32, device=dev)
+    lib = nat.load()
+    ws = torch.empty(int(lib.mgq_gptq_mxfp_workspace_size(B, R, C)), dtype=torch.uint8, device=dev)
+    offs = MXFP4_OFFSETS if mode == "mxfp4" else MXFP8_OFFSETS
+    offs_arr = (ctypes.c_int32 * len(offs))(*offs)  # alive until the call returns
+    nat.call(
+        "mgq_gptq_mxfp", W_in.data_ptr(), nat.dtype_code(W_in.dtype), B, R, C, H.data_ptr(),
+        nat.mode_code(mode), 1 if algorithm == "safe-scale-search" else 0, float(damp), 6,
+        ctypes.addressof(offs_arr), len(offs), q.data_ptr(), scales.data_ptr(), W_out.data_ptr(),
+        None if rel is None else rel.data_ptr(), att.data_ptr(), ws.data_ptr(), ws.numel(),
+        nat.stream_of(dev),
+    )
+    att_h = att.cpu().numpy()  # one small D2H copy: escalation warnings / failure
+    G = C // MX_GROUP_SIZE
+    for g in range(G):
+        sl = slice(g * MX_GROUP_SIZE, (g + 1) * MX_GROUP_SIZE)
+        _escalation_report(att_h[g], B, damp, 6,
+                           lambda idx, sl=sl: H[torch.as_tensor(idx, device=dev)][:, sl, sl])
+    return q, scales, rel
+
+
+@torch.no_grad()
+def _gptq_quantize_mxfp_groupwise(W: torch.Tensor, H: torch.Tensor, mode: str, damp: float,
+                                  algorithm: str):
+    """GPTQ independently inside each native 32-value group (gptq.py:69-180).
+
+    W float32 [B, R, C] is overwritten with the dequantized weights.
+    Returns (q uint8, scales uint8 E8M0, None, W, None).
+    """
+    if algorithm not in ("groupwise", "safe-scale-search"):
+        raise ValueError(f"unsupported MXFP GPTQ algorithm: {algorithm}")
+    _require_device(W, H)
+    q, scales, _ = _mxfp_solve(W, H, mode, damp, algorithm, W, False)
+    return q, scales, None, W, None
+
+
+def _require_device(W: torch.Tensor, H: torch.Tensor) -> None:
+    nat.device_for(W, H)
+    if not (W.is_cuda and H.is_cuda):
+        raise RuntimeError(
+            "mlx_gptq (MI355X build) solves on HIP devices only; move W and H to a "
+            "cuda (HIP) device first"
+        )
+    if W.device != H.device:
+        raise RuntimeError(f"W on {W.device} but H on {H.device}")
+    if H.dtype != torch.float32 or not H.is_contiguous():
+        raise TypeError("H must be a contiguous float32 tensor")
+    if not W.is_contiguous():
+        raise TypeError("W must be contiguous")
+
+
+@torch.no_grad()
+def gptq_quantize(
+    W: torch.Tensor,
+    H: torch.Tensor,
+    bits: int,
+    group_size: int,
+    damp: float = 0.01,
+    clip: str = "mse",
+    storage_dtype: torch.dtype = torch.bfloat16,
+    block_size: int = 128,
+    mode: str = "affine",
+    mxfp_algorithm: str = "auto",
+):
+    """Quantize W (in-place error compensation) against Hessian H (gptq.py:183-272).
+
+    W: [B, out, in] float32 (overwritten with the dequantized weights),
+    H: [B, in, in] float32 (dead-column diagonals set to 1 in place).
+    Returns (q uint8, scales, biases | None, W_dq (= W), None).
+    """
+    assert W.dim() == 3 and H.dim() == 3
+    B, R, C = W.shape
+    assert H.shape == (B, C, C)
+    assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
+    if mode in ("mxfp4", "mxfp8") and group_size != MX_GROUP_SIZE:
+        raise ValueError(f"{mode} requires group size {MX_GROUP_SIZE}")
+    if mode in ("mxfp4", "mxfp8"):
+        if mxfp_algorithm == "auto":
+            mxfp_algorithm = "safe-scale-search" if mode == "mxfp4" else "groupwise"
+        if W.dtype != torch.float32:
+            raise TypeError("gptq_quantize updates W in place and needs float32 W")
+        return _gptq_quantize_mxfp_groupwise(W, H, mode, damp, mxfp_algorithm)
+    if mode != "affine":
+        raise ValueError(f"unsupported quantization mode: {mode}")
+    from . import gptq_affine
+
+    return gptq_affine.gptq_quantize_affine(W, H, bits, group_size, damp, clip, storage_dtype,
+                                            block_size)
+
+
+@torch.no_grad()
+def solve_gptq(
+    W_orig: torch.Tensor,
+    H: torch.Tensor,
+    bits: int,
+    group_size: int,
+    damp: float = 0.01,
+    clip: str = "mse",
+    storage_dtype: torch.dtype = torch.bfloat16,
+    mode: str = "affine",
+    mxfp_algorithm: str = "auto",
+):
+    """Keep W_orig intact, return (q, scales, biases, W_dq, rel_err[B]) (gptq.py:275-302)."""
+    if mode in ("mxfp4", "mxfp8"):
+        assert W_orig.dim() == 3 and H.dim() == 3
+        B, R, C = W_orig.shape
+        assert H.shape == (B, C, C)
+        assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
+        if group_size != MX_GROUP_SIZE:
+            raise ValueError(f"{mode} requires group size {MX_GROUP_SIZE}")
+        if mxfp_algorithm == "auto":
+            mxfp_algorithm = "safe-scale-search" if mode == "mxfp4" else "groupwise"
+        src = W_orig if W_orig.dtype in (torch.float32, torch.bfloat16, torch.float16) else W_orig.float()
+        src = src.contiguous()
+        _require_device(src, H)
+        W_dq = torch.empty(B, R, C, dtype=torch.float32, device=src.device)
+        q, s, rel = _mxfp_solve(src, H, mode, damp, mxfp_algorithm, W_dq, True)
+        return q, s, None, W_dq, rel
+    W = W_orig.float().clone()
+    q, s, b, W_dq, _ = gptq_quantize(W, H, bits, group_size, damp=damp, clip=clip,
+                                     storage_dtype=storage_dtype, mode=mode,
+                                     mxfp_algorithm=mxfp_algorithm)
+    from . import gptq_affine
+
+    return q, s, b, W_dq, gptq_affine.rel_err(W_dq, W_orig)
