@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Benchmark: one MoE layer of GPTQ calibration on one MI355X.
+
+Workload (the north-star target): a
+Qwen3-30B-A3B-shaped MoE layer -- 128 experts, hidden 2048,
+moe_intermediate 768, 131072 tokens routed top-8 -- solved end to end:
+  per-expert Hessians (gate_up: routed gather of the hidden states, 2048^2;
+  down: the experts' SiLU(g)*u inputs, 768^2), damped per-group Cholesky
+  inverses, MXFP4 safe-scale-search GPTQ for every routed expert, RTN for
+  the 4 unrouted experts (they have no Hessian), and MLX uint32 packing of
+  all codes. Inputs (hidden states, routing, expert weights) are synthetic,
+  seeded, and resident in HBM before the timed region.
+
+One step = one layer. The JSON line reports weight elements solved per
+second, the Hessian kernel against the bf16 MFMA roofline, and the CPU
+oracle (the reference algorithm restated on torch-CPU) timed on a bounded
+sample of experts of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mlx-gptq-mxfp_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def _args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="time budget of the CPU-oracle sample (0 disables it)")
+    return ap.parse_args(argv)
+
+
+def _hessian_traffic():
+    """HBM bytes per Hessian launch measured with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE, if the profile summary is present (profiles/)."""
+    p = os.path.join(ROOT, "profiles", "hessian_moe_cfg4_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def main(argv=None) -> int:
+    args = _args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures a single GPU (got --gpus {args.gpus}); multi-GPU runs are out of "
+              "scope for this build (experts shard across GPUs with no exchange)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from mlx_gptq import _native, capture, gptq, grid, packing, synth
+
+    _native.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    t_setup = time.perf_counter()
+    L = synth.moe_layer(device=dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    E, ne = L.experts, L.experts - L.n_empty
+    hidden, inter = L.W_gate_up.shape[2], L.W_down.shape[2]
+    counts = L.counts()
+    assert all(c > 0 for c in counts[:ne]) and all(c == 0 for c in counts[ne:])
+    A = L.offsets[-1]
+    elements = E * (2 * inter * hidden + hidden * inter)
+
+    H_gu = torch.empty(E, hidden, hidden, dtype=torch.float32, device=dev)
+    H_dn = torch.empty(E, inter, inter, dtype=torch.float32, device=dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+
+    def step():
+        evs[0].record()
+        capture.grouped_hessian(L.X, L.offsets, L.row_index, out=H_gu, validate=False)
+        evs[1].record()
+        capture.grouped_hessian(L.Y, L.offsets, out=H_dn)
+        evs[2].record()
+        q_gu, s_gu, _, wq_gu, _ = gptq.solve_gptq(L.W_gate_up[:ne], H_gu[:ne], 4, 32, mode="mxfp4")
+        evs[3].record()
+        q_dn, s_dn, _, wq_dn, _ = gptq.solve_gptq(L.W_down[:ne], H_dn[:ne], 4, 32, mode="mxfp4")
+        evs[4].record()
+        rq_gu, rs_gu, _, _ = grid.rtn_quantize_mxfp(L.W_gate_up[ne:], "mxfp4")
+        rq_dn, rs_dn, _, _ = grid.rtn_quantize_mxfp(L.W_down[ne:], "mxfp4")
+        packed = [packing.pack_q(q, 4) for q in (q_gu, q_dn, rq_gu, rq_dn)]
+        evs[5].record()
+        return q_gu, s_gu, q_dn, s_dn, packed
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    phase = np.zeros(5)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+        torch.cuda.synchronize()  # events of this step are complete
+        phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(5)]
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    phase /= args.steps
+    value = elements / (ms_step * 1e-3)
+
+    hess_flops = A * hidden * (hidden + 1)  # SYRK count N*C*(C+1), gate_up launch
+    hess_ms = float(phase[0])
+    achieved = hess_flops / (hess_ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": "syrk_tile_kernel (gate_up Hessian, routed gather)",
+        "bound": "mfma",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": _hessian_traffic(),
+        "flops_per_launch": hess_flops,
+        "launch_ms": round(hess_ms, 4),
+    }
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = _cpu_baseline(L, ne, out, args.cpu_seconds)
+
+    line = {
+        "metric": "GPTQ weight-elements solved/s per layer",
+        "value": round(value, 1),
+        "unit": "elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16-mfma+fp32",
+        "data": "synthetic (seeded hidden states, router, expert weights)",
+        "config": {
+            "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
+                        "[2048,768]), 131072 tokens top-8, MXFP4 safe-scale-search GPTQ, 4 unrouted "
+                        "experts RTN, uint32 pack",
+            "experts": E, "hidden": hidden, "moe_intermediate": inter, "tokens": L.X.shape[0],
+            "top_k": A // L.X.shape[0], "assignments": A, "elements": elements,
+        },
+        "phases_ms": {"hessian_gate_up": round(float(phase[0]), 3), "hessian_down": round(float(phase[1]), 3),
+                      "solve_gate_up": round(float(phase[2]), 3), "solve_down": round(float(phase[3]), 3),
+                      "rtn_and_pack": round(float(phase[4]), 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _cpu_baseline(L, ne, gpu_out, budget_s):
+    """Time the CPU oracle on whole experts of the same layer until the budget
+    is spent; also report code agreement with the GPU on those experts."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import gptq_ref, hessian_ref, packing_ref
+
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    hidden, inter = L.W_gate_up.shape[2], L.W_down.shape[2]
+    q_gu, _, q_dn, _, _ = gpu_out
+    spent, done, elems, agree_n, agree_d = 0.0, 0, 0, 0, 0
+    # spread the sample over the expert range (light and heavy experts)
+    order = list(range(0, ne, 7)) + [e for e in range(ne) if e % 7]
+    for e in order:
+        a, b = L.offsets[e], L.offsets[e + 1]
+        xs = L.X.index_select(0, L.row_index[a:b].long()).cpu()
+        ys = L.Y[a:b].cpu()
+        wg = L.W_gate_up[e : e + 1].cpu()
+        wd = L.W_down[e : e + 1].cpu()
+        t = time.perf_counter()
+        Hg = hessian_ref.stash_hessian([xs], hidden)
+        Hd = hessian_ref.stash_hessian([ys], inter)
+        rq_g, _, _, _, _ = gptq_ref.solve_gptq(wg, Hg.unsqueeze(0), 4, 32, mode="mxfp4")
+        rq_d, _, _, _, _ = gptq_ref.solve_gptq(wd, Hd.unsqueeze(0), 4, 32, mode="mxfp4")
+        packing_ref.pack_q(rq_g.numpy(), 4)
+        packing_ref.pack_q(rq_d.numpy(), 4)
+        spent += time.perf_counter() - t
+        done += 1
+        elems += wg.numel() + wd.numel()
+        agree_n += int((q_gu[e].cpu() == rq_g[0]).sum()) + int((q_dn[e].cpu() == rq_d[0]).sum())
+        agree_d += rq_g.numel() + rq_d.numel()
+        if spent >= budget_s:
+            break
+    return {
+        "value": round(elems / spent, 1),
+        "unit": "elements/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {ne} routed experts of the same layer (gate_up + down each): CPU oracle "
+                  f"Hessian (fp32 addmm) + Cholesky + MXFP4 safe-search GPTQ + pack, {spent:.1f} s",
+        "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())
