@@ -24,9 +24,12 @@ namespace {
 constexpr int kN = 32;
 
 // attempts[g*B + b]: 1..max_attempts on success, 0 if every attempt failed.
+// sym[b*G + g] (optional): 1 when the undamped block is exactly symmetric.
+// Hc (optional): compact [B*G][32][32] copy of each undamped block.
 __global__ void __launch_bounds__(64)
     hinv32_kernel(const float* __restrict__ H, int64_t B, int64_t C, float damp,
-                  int max_attempts, float* __restrict__ U, int32_t* __restrict__ attempts) {
+                  int max_attempts, float* __restrict__ U, int32_t* __restrict__ attempts,
+                  uint8_t* __restrict__ sym, float* __restrict__ Hc) {
   __shared__ double A[kN][kN + 1];
   __shared__ double Wm[kN][kN + 1];
   const int64_t G = C / kN;
@@ -40,6 +43,21 @@ __global__ void __launch_bounds__(64)
   for (int i = 0; i < kN; ++i) dsum += static_cast<double>(Hb[static_cast<int64_t>(i) * C + i]);
   float dmean = static_cast<float>(dsum / kN);
   dmean = (dmean < 1e-8f) ? 1e-8f : dmean;  // NaN stays NaN
+
+  if (Hc) {
+    float* dst = Hc + (b * G + g) * kN * kN;
+    for (int e = lane; e < kN * kN; e += 64) dst[e] = Hb[static_cast<int64_t>(e / kN) * C + e % kN];
+  }
+  if (sym) {
+    bool same = true;
+    for (int e = lane; e < kN * kN; e += 64) {
+      const int i = e / kN, j = e % kN;
+      same = same && (__float_as_uint(Hb[static_cast<int64_t>(i) * C + j]) ==
+                      __float_as_uint(Hb[static_cast<int64_t>(j) * C + i]));
+    }
+    const bool all_same = __all(same);
+    if (lane == 0) sym[b * G + g] = all_same ? 1 : 0;
+  }
 
   float cur = damp;
   int used = 0;
@@ -109,11 +127,11 @@ __global__ void __launch_bounds__(64)
 
 // Launch helper shared with the MXFP solver.
 int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, hipStream_t s) {
+                  int32_t* attempts, uint8_t* sym, float* Hc, hipStream_t s) {
   const int64_t G = C / kN;
   if (B * G == 0) return MGQ_OK;
   hinv32_kernel<<<static_cast<unsigned>(B * G), 64, 0, s>>>(H, B, C, damp, max_attempts, U,
-                                                          attempts);
+                                                          attempts, sym, Hc);
   return check_launch("hinv32");
 }
 
@@ -129,5 +147,6 @@ extern "C" int mgq_prepare_hinv_blocks(const float* H, int64_t B, int64_t C, int
   MGQ_REQUIRE(B >= 0 && C >= 0 && C % kN == 0, MGQ_ERR_SHAPE,
               "C=%lld not a multiple of the block size %d", (long long)C, kN);
   MGQ_REQUIRE(max_attempts >= 1, MGQ_ERR_VALUE, "max_attempts must be >= 1");
-  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, as_stream(stream));
+  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, nullptr, nullptr,
+                       as_stream(stream));
 }

@@ -29,7 +29,7 @@
 namespace mgq {
 
 int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, hipStream_t s);
+                  int32_t* attempts, uint8_t* sym, float* Hc, hipStream_t s);
 
 namespace {
 
@@ -57,58 +57,113 @@ __global__ void dead_fix_kernel(float* __restrict__ H, int64_t B, int64_t C,
   }
 }
 
+// Exact reference projection of one element (code and dq), w / scale done
+// as w * inv_scale (identical for power-of-two scales).
 template <int MODE>
-__device__ inline float quant_dq(float w, float scale, uint32_t* code) {
-  float dq;
-  *code = mx_quant(w, scale, MODE, &dq);
-  return dq;
+__device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, float* dq) {
+  const float n = w * inv_scale;
+  uint32_t code;
+  float v;
+  if (MODE == kMxfp4) {
+    code = e2m1_code(n);
+    v = e2m1_value(code);
+  } else {
+    code = e4m3_code_clamped(clamp448(n));
+    v = e4m3_value(code);
+  }
+  *dq = v * scale;
+  return code;
 }
 
-// e^T Hg e. Hg row stride C; values are wave-uniform (scalar loads).
-// Symmetric blocks use the upper triangle (H_ii e_i^2 + 2 sum_{j>i} H_ij e_i e_j
-// as e_i * (H_ii e_i + 2 * sum_{j>i} H_ij e_j)); otherwise the full form.
-__device__ inline float quad_form(const float (&e)[kG], const float* __restrict__ Hg, int64_t C,
-                                  bool sym) {
+template <int MODE>
+__device__ inline float quant_fast(float w, float inv_scale, float scale) {
+  return MODE == kMxfp4 ? mx4_dq(w, inv_scale, scale) : mx8_dq(w, inv_scale, scale);
+}
+
+// e^T Hg e with fused multiply-adds in a fixed order. Hg is the block's
+// compact [32][32] copy (row stride 32), wave-uniform, so every element is a
+// scalar load at a compile-time offset from one base pointer. Symmetric
+// blocks use the upper triangle: sum_i e_i * (H_ii e_i + 2 sum_{j>i} H_ij e_j).
+__device__ inline float quad_form(const float (&e)[kG], const float* __restrict__ Hg, bool sym) {
   float obj = 0.0f;
   if (sym) {
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      float s = 0.0f;
+      float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-      for (int j = i + 1; j < kG; ++j) s += Hg[i * C + j] * e[j];
-      const float t = Hg[i * C + i] * e[i] + 2.0f * s;
-      obj += e[i] * t;
+      for (int j = i + 1; j < kG; j += 2) {
+        s0 = fmaf(Hg[i * kG + j], e[j], s0);
+        if (j + 1 < kG) s1 = fmaf(Hg[i * kG + j + 1], e[j + 1], s1);
+      }
+      obj = fmaf(e[i], fmaf(Hg[i * kG + i], e[i], 2.0f * (s0 + s1)), obj);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      float t = 0.0f;
+      float t0 = 0.0f, t1 = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kG; ++j) t += Hg[i * C + j] * e[j];
-      obj += e[i] * t;
+      for (int j = 0; j < kG; j += 2) {
+        t0 = fmaf(Hg[i * kG + j], e[j], t0);
+        t1 = fmaf(Hg[i * kG + j + 1], e[j + 1], t1);
+      }
+      obj = fmaf(e[i], t0 + t1, obj);
     }
   }
   return obj;
 }
 
+// An opaque zero that depends on `v`: addresses built from it cannot be
+// computed before `v`, so the loads behind them are neither hoisted out of
+// the candidate loop nor scheduled far ahead of their use. Without this the
+// compiler lifts the 528 Hessian values (or the U block) out of the loops and
+// runs out of registers. zero_after_s gives a wave-uniform (scalar) zero so
+// the Hessian reads stay scalar loads.
+__device__ inline int zero_after(float v) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(v));
+  return z;
+}
+__device__ inline int zero_after_s(float v) { return __builtin_amdgcn_readfirstlane(zero_after(v)); }
+
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 
-template <typename T>
-__device__ inline float load_w(const T* p, int i);
-template <>
-__device__ inline float load_w<float>(const float* p, int i) { return p[i]; }
-template <>
-__device__ inline float load_w<uint16_t>(const uint16_t* p, int i) { return bf16_to_f32(p[i]); }
-
-struct F16Tag {};
+// The 32 weights of one (row, group), 16-byte loads, widened to fp32.
+template <typename TIn, bool IS_F16>
+__device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float (&v)[kG]) {
+  if constexpr (sizeof(TIn) == 4) {
+    const float4* p = reinterpret_cast<const float4*>(W + base);
+#pragma unroll
+    for (int i = 0; i < kG / 4; ++i) {
+      const float4 x = p[i];
+      v[4 * i] = x.x;
+      v[4 * i + 1] = x.y;
+      v[4 * i + 2] = x.z;
+      v[4 * i + 3] = x.w;
+    }
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(W + base);
+#pragma unroll
+    for (int i = 0; i < kG / 8; ++i) {
+      const uint4 x = p[i];
+      const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t lo = static_cast<uint16_t>(d[k] & 0xffffu);
+        const uint16_t hi = static_cast<uint16_t>(d[k] >> 16);
+        v[8 * i + 2 * k] = IS_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+        v[8 * i + 2 * k + 1] = IS_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+      }
+    }
+  }
+}
 
 template <typename TIn, bool IS_F16, int MODE, bool SAFE>
 __global__ void __launch_bounds__(kThreads)
     mxfp_solve_kernel(const TIn* __restrict__ W, int64_t B, int64_t R, int64_t C,
-                      const float* __restrict__ H, const float* __restrict__ U,
-                      const uint8_t* __restrict__ dead, Offsets offs, uint8_t* __restrict__ q_out,
-                      uint8_t* __restrict__ s_out, float* __restrict__ W_dq,
-                      double* __restrict__ rel_part) {
+                      const float* __restrict__ Hc, const float* __restrict__ U,
+                      const uint8_t* __restrict__ dead, const uint8_t* __restrict__ symflag,
+                      Offsets offs, uint8_t* __restrict__ q_out, uint8_t* __restrict__ s_out,
+                      float* __restrict__ W_dq, double* __restrict__ rel_part) {
   const int64_t G = C / kG;
   const int64_t chunks = (R + kThreads - 1) / kThreads;
   const int64_t bg = blockIdx.x / chunks;
@@ -118,36 +173,34 @@ __global__ void __launch_bounds__(kThreads)
   const bool valid = r_raw < R;
   const int64_t r = valid ? r_raw : R - 1;
 
-  const float* __restrict__ Hg = H + b * C * C + (g * kG) * C + g * kG;
-  const float* __restrict__ Ug = U + (b * G + g) * kG * kG;
+  // compact (post dead-column fix) Hessian block, written by hinv32
+  const float* __restrict__ Hg = Hc + (b * G + g) * kG * kG;
+  // U^T staged in LDS (Ut[c][k] = U[k][c]): the recurrence below reads one
+  // column of U per step with broadcast LDS loads (uniform addresses).
+  __shared__ float Ut[kG * kG];
+  {
+    const float* Ub = U + (b * G + g) * kG * kG;
+    for (int e = threadIdx.x; e < kG * kG; e += kThreads) Ut[(e % kG) * kG + e / kG] = Ub[e];
+  }
+  __syncthreads();
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
   const int64_t base = (b * R + r) * C + g * kG;
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
+  const bool sym = symflag[b * G + g] != 0;
 
-  // symmetric Hessian block? (uniform; exact bit equality)
-  bool sym = true;
-  if (SAFE) {
+  float orig[kG];
+  load_group<TIn, IS_F16>(W, base, orig);
+  {  // dead columns (gptq.py:219-221) read as 0
+    const uint4 m0 = reinterpret_cast<const uint4*>(dd)[0];
+    const uint4 m1 = reinterpret_cast<const uint4*>(dd)[1];
+    const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
     for (int i = 0; i < kG; ++i)
-#pragma unroll
-      for (int j = i + 1; j < kG; ++j)
-        sym = sym && (__float_as_uint(Hg[i * C + j]) == __float_as_uint(Hg[j * C + i]));
+      if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) orig[i] = 0.0f;
   }
-
-  float raw[kG], orig[kG];
-  float amax = 0.0f;
+  float amax = fabsf(orig[0]);
 #pragma unroll
-  for (int i = 0; i < kG; ++i) {
-    float v;
-    if constexpr (IS_F16) {
-      v = f16_to_f32(reinterpret_cast<const uint16_t*>(W)[base + i]);
-    } else {
-      v = load_w<TIn>(W + base, i);
-    }
-    raw[i] = v;
-    orig[i] = dd[i] ? 0.0f : v;
-    amax = (i == 0) ? fabsf(orig[i]) : nan_max(amax, fabsf(orig[i]));
-  }
+  for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(orig[i]));
 
   // 1. scale choice
   const int e0 = e8m0_exponent(amax, fmax);
@@ -158,35 +211,37 @@ __global__ void __launch_bounds__(kThreads)
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
-      const float sc = exp2_int(e);
+      const float sc = exp2_int(e), inv = exp2_int(-e);
 #pragma unroll
-      for (int i = 0; i < kG; ++i) {
-        uint32_t code;
-        err[i] = quant_dq<MODE>(orig[i], sc, &code) - orig[i];
-      }
-      const float obj = quad_form(err, Hg, C, sym);
+      for (int i = 0; i < kG; ++i) err[i] = quant_fast<MODE>(orig[i], inv, sc) - orig[i];
+      const float obj = quad_form(err, Hg + zero_after_s(err[0]), sym);
       if (o == 0 || obj < best) {
         best = obj;
         e_sel = e;
       }
     }
   }
-  const float scale = exp2_int(e_sel);
+  const float scale = exp2_int(e_sel), inv_scale = exp2_int(-e_sel);
 
-  // 2. GPTQ recurrence with the fixed scale; w[c] becomes dq_c.
-  float w[kG];
+  // 2. GPTQ recurrence with the fixed scale, column by column. The
+  // reference updates all later columns after each step
+  // (W[c+1:] -= err_c * U[c, c+1:]); each element therefore sees
+  // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
+  // Forming w_c lazily from the stored errors performs exactly those
+  // roundings while keeping only err[] live.
+  float w[kG], errs[kG];
   uint32_t codes[kG / 4];
-#pragma unroll
-  for (int i = 0; i < kG; ++i) w[i] = orig[i];
 #pragma unroll
   for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
   for (int c = 0; c < kG; ++c) {
-    uint32_t code;
-    const float dq = quant_dq<MODE>(w[c], scale, &code);
-    const float err = (w[c] - dq) / Ug[c * kG + c];
+    const float* col = Ut + c * kG + (c ? zero_after(errs[c - 1]) : 0);
+    float acc = orig[c];
 #pragma unroll
-    for (int j = c + 1; j < kG; ++j) w[j] = w[j] - err * Ug[c * kG + j];
+    for (int k = 0; k < c; ++k) acc = acc - errs[k] * col[k];
+    float dq;
+    const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
+    errs[c] = (acc - dq) / col[c];
     w[c] = dq;
     codes[c / 4] |= code << (8 * (c % 4));
   }
@@ -197,7 +252,7 @@ __global__ void __launch_bounds__(kThreads)
     float err[kG];
 #pragma unroll
     for (int i = 0; i < kG; ++i) err[i] = w[i] - orig[i];
-    use_gptq = quad_form(err, Hg, C, sym) <= best;
+    use_gptq = quad_form(err, Hg + zero_after_s(err[kG - 1]), sym) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;
@@ -213,25 +268,37 @@ __global__ void __launch_bounds__(kThreads)
     for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      uint32_t code;
-      w[i] = quant_dq<MODE>(orig[i], scale, &code);
+      const uint32_t code = quant_exact<MODE>(orig[i], inv_scale, scale, &w[i]);
       codes[i / 4] |= code << (8 * (i % 4));
     }
   }
 
   double num = 0.0, den = 0.0;
   if (valid) {
-    uint32_t* qp = reinterpret_cast<uint32_t*>(q_out + base);
+    uint4* qp = reinterpret_cast<uint4*>(q_out + base);
+    qp[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+    qp[1] = make_uint4(codes[4], codes[5], codes[6], codes[7]);
+    float4* op = reinterpret_cast<float4*>(W_dq + base);
 #pragma unroll
-    for (int i = 0; i < kG / 4; ++i) qp[i] = codes[i];
-#pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      W_dq[base + i] = w[i];
-      const double d = static_cast<double>(w[i]) - static_cast<double>(raw[i]);
-      num += d * d;
-      den += static_cast<double>(raw[i]) * static_cast<double>(raw[i]);
-    }
+    for (int i = 0; i < kG / 4; ++i)
+      op[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
     s_out[(b * R + r) * G + g] = static_cast<uint8_t>(e_sel + 127);
+    if (rel_part) {
+      // rel_err against the caller's W as given, dead columns included
+      // (gptq.py:300-302). W does not alias W_dq when rel_err is requested
+      // (checked on the host), so re-reading it here is safe and keeps 32
+      // registers free during the solve.
+      float raw[kG];
+      // opaque offset: a fresh load after the solve, not the first load's
+      // registers kept alive through it
+      load_group<TIn, IS_F16>(W, base + zero_after(w[kG - 1]), raw);
+#pragma unroll
+      for (int i = 0; i < kG; ++i) {
+        const double d = static_cast<double>(w[i]) - static_cast<double>(raw[i]);
+        num += d * d;
+        den += static_cast<double>(raw[i]) * static_cast<double>(raw[i]);
+      }
+    }
   }
   if (rel_part) {
     // wave reduction, one (num, den) pair per wave
@@ -281,7 +348,7 @@ __global__ void rel_err_kernel(const double* __restrict__ part, int64_t n_per_b,
 }
 
 struct WsLayout {
-  int64_t dead_off, u_off, rel_off, total;
+  int64_t dead_off, sym_off, u_off, hc_off, rel_off, total;
 };
 
 WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
@@ -289,22 +356,24 @@ WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
   const int64_t G = C / kG;
   WsLayout L;
   L.dead_off = 0;
-  L.u_off = al(B * C);
-  L.rel_off = L.u_off + al(B * G * kG * kG * 4);
+  L.sym_off = al(B * C);
+  L.u_off = L.sym_off + al(B * G);
+  L.hc_off = L.u_off + al(B * G * kG * kG * 4);
+  L.rel_off = L.hc_off + al(B * G * kG * kG * 4);
   L.total = L.rel_off + al(B * G * ((R + 63) / 64) * 2 * 8);
   return L;
 }
 
 template <typename TIn, bool IS_F16>
-int launch_solve(const void* W, int64_t B, int64_t R, int64_t C, const float* H, const float* U,
-                 const uint8_t* dead, int mode, bool safe, const Offsets& offs, uint8_t* q,
+int launch_solve(const void* W, int64_t B, int64_t R, int64_t C, const float* Hc, const float* U,
+                 const uint8_t* dead, const uint8_t* sym, int mode, bool safe, const Offsets& offs, uint8_t* q,
                  uint8_t* s, float* W_dq, double* rel_part, hipStream_t st) {
   const int64_t G = C / kG;
   const int64_t blocks = B * G * ((R + kThreads - 1) / kThreads);
   const TIn* w = static_cast<const TIn*>(W);
 #define MGQ_LAUNCH(MODE, SAFE)                                                              \
   mxfp_solve_kernel<TIn, IS_F16, MODE, SAFE><<<static_cast<unsigned>(blocks), kThreads, 0, st>>>( \
-      w, B, R, C, H, U, dead, offs, q, s, W_dq, rel_part)
+      w, B, R, C, Hc, U, dead, sym, offs, q, s, W_dq, rel_part)
   if (mode == kMxfp4) {
     if (safe) MGQ_LAUNCH(kMxfp4, true); else MGQ_LAUNCH(kMxfp4, false);
   } else {
@@ -351,26 +420,34 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
   MGQ_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MGQ_ERR_WORKSPACE,
               "mxfp workspace %lld < %lld bytes", (long long)workspace_bytes,
               (long long)L.total);
+  MGQ_REQUIRE(rel_err == nullptr || static_cast<const void*>(W_dq) != W, MGQ_ERR_VALUE,
+              "rel_err needs W_dq separate from W (in-place solves skip rel_err)");
+  MGQ_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(W_dq) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0,
+              MGQ_ERR_SHAPE, "W, W_dq and q_out must be 16-byte aligned");
   if (B == 0 || C == 0) return MGQ_OK;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   uint8_t* dead = reinterpret_cast<uint8_t*>(ws + L.dead_off);
+  uint8_t* sym = reinterpret_cast<uint8_t*>(ws + L.sym_off);
   float* U = reinterpret_cast<float*>(ws + L.u_off);
+  float* Hcmp = reinterpret_cast<float*>(ws + L.hc_off);
   double* rel_part = reinterpret_cast<double*>(ws + L.rel_off);
 
   dead_fix_kernel<<<elementwise_blocks(B * C, 256), 256, 0, st>>>(H, B, C, dead);
   if (int rc = check_launch("dead-column fix")) return rc;
-  if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, st)) return rc;
+  if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, sym, Hcmp, st)) return rc;
   if (R == 0) return MGQ_OK;
   int rc;
   if (w_dtype == kF32) {
-    rc = launch_solve<float, false>(W, B, R, C, H, U, dead, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<float, false>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
                                     scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else if (w_dtype == kBF16) {
-    rc = launch_solve<uint16_t, false>(W, B, R, C, H, U, dead, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<uint16_t, false>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
                                        scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else {
-    rc = launch_solve<uint16_t, true>(W, B, R, C, H, U, dead, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<uint16_t, true>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
                                       scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   }
   if (rc) return rc;

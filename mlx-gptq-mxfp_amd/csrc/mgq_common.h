@@ -183,6 +183,55 @@ __device__ inline uint32_t mx_quant(float w, float scale, int mode, float* dq) {
 }
 
 // ---------------------------------------------------------------------------
+// Solver fast path: the same values as mx_quant, computed arithmetically.
+// Because every MXFP scale is a power of two, w / scale == w * (1/scale)
+// exactly (both are the correctly rounded w * 2^-e, and 2^-e is
+// representable for e in [-127, 127]). These produce exactly mx_quant's dq
+// (same grid value, same sign rule, same product with the scale) without
+// materialising the code; the solver uses them to score scale candidates.
+// ---------------------------------------------------------------------------
+
+// E2M1 magnitude of |n| (RNE on {0,.5,1,1.5,2,3,4,6}, saturating), 0 for NaN.
+// Below 2 the grid step is 1/2, on [2,4) it is 1, from 4 it is 2: scaling by
+// the inverse step makes the grid the integers, where rint is exactly the
+// reference's threshold chain (ties to the even code).
+__device__ inline float e2m1_mag(float ax) {
+  const float f = ax < 2.0f ? 2.0f : (ax < 4.0f ? 1.0f : 0.5f);
+  const float finv = ax < 2.0f ? 0.5f : (ax < 4.0f ? 1.0f : 2.0f);
+  const float q = fminf(rintf(ax * f) * finv, 6.0f);
+  return (ax == ax) ? q : 0.0f;
+}
+
+// Signed dequantized MXFP4 value dq = value(code(n)) * scale, n = w * inv_scale.
+// The sign is the reference's code sign bit (n < 0), so (-0.25, 0) -> -0.0.
+__device__ inline float mx4_dq(float w, float inv_scale, float scale) {
+  const float n = w * inv_scale;
+  const float m = e2m1_mag(fabsf(n));
+  return (n < 0.0f ? -m : m) * scale;
+}
+
+// E4M3 value of clamp(n, +-448) rounded half-even onto the e4m3fn grid,
+// sign preserved, NaN stays NaN.
+__device__ inline float e4m3_round(float n) {
+  const uint32_t u = __float_as_uint(n);
+  const uint32_t sign = u & 0x80000000u;
+  uint32_t ua = u & 0x7fffffffu;
+  if (ua > 0x7f800000u) return __uint_as_float(sign | 0x7fc00000u);
+  if (ua > 0x43e00000u) ua = 0x43e00000u;  // 448
+  float m;
+  if (ua < 0x3c800000u) {  // below 2^-6: subnormal step 2^-9
+    m = rintf(__uint_as_float(ua) * 512.0f) * 0.001953125f;
+  } else {
+    m = __uint_as_float((ua + 0x7ffffu + ((ua >> 20) & 1u)) & 0xfff00000u);
+  }
+  return __uint_as_float(__float_as_uint(m) | sign);
+}
+
+__device__ inline float mx8_dq(float w, float inv_scale, float scale) {
+  return e4m3_round(w * inv_scale) * scale;
+}
+
+// ---------------------------------------------------------------------------
 // Small helpers.
 // ---------------------------------------------------------------------------
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
