@@ -212,6 +212,43 @@ int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, f
                   float* rel_err, int32_t* attempts, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* Workspace bytes needed by mgq_hinv_full_pass for H [B, C, C] (two fp64
+ * [B, C, C] arrays). */
+int64_t mgq_hinv_full_workspace_size(int64_t B, int64_t C);
+
+/* One damping attempt of gptq.py:27-66 _prepare_hinv on full [C, C]
+ * matrices (the affine solver's factor, gptq.py:229): for every item with
+ * active[b] != 0, U[b] (f32 upper, zero below the diagonal) with
+ *   U^T U = (H[b] + lam_b I)^-1,  lam_b = damp[b] * max(mean(diag H[b]), 1e-8).
+ * Factorisation and inverse run in fp64 (blocked UL Cholesky, nb = 64) and
+ * are rounded to f32 once. failed[b] is set to 1 (and U[b] left unwritten)
+ * when a pivot is <= 0 or NaN; the caller clears failed[] before the call.
+ * The reference's escalation (damp x10 for the failed items only, up to 6
+ * attempts) is the caller's loop over this pass with active = failed.
+ * damp: f32 [B], active/failed: u8 [B], all device. */
+int mgq_hinv_full_pass(const float* H, int64_t B, int64_t C, const float* damp,
+                       const uint8_t* active, uint8_t* failed, float* U, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* gptq.py:216-222: dead columns (diag(H) <= 0) are zeroed in W f32
+ * [B, R, C] (W may be NULL) and their H diagonal set to 1, in place. */
+int mgq_dead_fix(float* W, int64_t B, int64_t R, int64_t C, float* H, void* stream);
+
+/* One lazy block [i1, i1 + n) of the affine column loop, gptq.py:241-270:
+ * every G-column group starts with grid.py:167-212 choose_qparams on the
+ * block-updated weights (scales/biases stored in storage_dtype at group
+ * index col / G), then each column is quantized (grid.py:215-221), its
+ * error e = (w - dq) / U[c, c] is propagated to the block's later columns
+ * and stored in Err; afterwards W[:, :, i1+n:] -= Err @ U[i1:i1+n, i1+n:]
+ * (gptq.py:269-270). W f32 [B, R, C] (columns of the block become dq),
+ * U f32 [B, C, C] from mgq_hinv_full_pass, q_out u8 [B, R, C],
+ * s_store / b_store [B, R, C/G] of storage_dtype, Err f32 [B, R, n].
+ * G <= 128, C, i1 and n multiples of G, n <= 2048. */
+int mgq_gptq_affine_block(float* W, const float* U, int64_t B, int64_t R, int64_t C, int64_t i1,
+                          int64_t n, int group_size, int bits, int method, int storage_dtype,
+                          int grid_steps, double max_shrink, uint8_t* q_out, void* s_store,
+                          void* b_store, float* Err, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

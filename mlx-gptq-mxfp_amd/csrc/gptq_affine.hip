@@ -1,0 +1,315 @@
+// Affine (MLX scale/bias) GPTQ: the lazy-block column loop of
+// gptq.py:229-272 with the MSE clip search of grid.py:167-212.
+//
+// One wavefront owns one (batch item, row). For each block of `bs` columns
+// (a multiple of the group size G) and each G-column group in it:
+//   - lane t holds column j+t (and j+t+64 for G = 128); at the group start
+//     the lane applies the earlier in-block updates
+//         w <- w - err_k * U[k, col]   for k = block start .. j-1, in order,
+//     which are exactly the element's updates in the reference's order;
+//   - the clip search runs on those G values across lanes (wave min/max and
+//     wave sums of squared errors, strict '<' over the shrink candidates);
+//   - the G columns are then quantized one by one; the owner lane's error
+//     err = (w - dq) / U[c, c] is broadcast and every later column applies
+//     w <- w - err * U[c, col].
+// After the block a separate kernel applies the deferred update
+//     W[:, i2:] -= Err @ U[i1:i2, i2:]
+// (the reference's bmm) as an fp32 GEMM.
+#include "mgq_capi.h"
+#include "mgq_common.h"
+
+namespace mgq {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kMaxBlock = 2048;  // errs of one block per wave in LDS: 32 KB
+constexpr int kMaxShrinks = 128;
+
+struct Shrinks {
+  int n;
+  float p_over_maxq[kMaxShrinks];
+  float p[kMaxShrinks];
+};
+
+__device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
+__device__ inline float nan_min(float m, float a) { return (a < m || a != a) ? a : m; }
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ inline float wave_nan_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = nan_min(v, __shfl_xor(v, off));
+  return v;
+}
+__device__ inline float wave_nan_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ inline float affine_q(float w, float b, float s_safe, float maxq) {
+  float q = rintf((w - b) / s_safe);
+  if (q != q) return q;
+  return fminf(fmaxf(q, 0.0f), maxq);
+}
+
+// gptq.py:216-222 for the affine path: dead columns zeroed in W, H diag := 1.
+__global__ void dead_fix_w_kernel(float* __restrict__ W, float* __restrict__ H, int64_t B,
+                                  int64_t R, int64_t C) {
+  const int64_t n = B * R * C;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i / (R * C), c = i % C;
+    if (H[b * C * C + c * C + c] <= 0.0f) W[i] = 0.0f;
+  }
+}
+
+__global__ void dead_fix_h_kernel(float* __restrict__ H, int64_t B, int64_t C) {
+  const int64_t n = B * C;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i / C, c = i % C;
+    float* d = H + b * C * C + c * C + c;
+    if (*d <= 0.0f) *d = 1.0f;
+  }
+}
+
+template <int CPL>
+__global__ void __launch_bounds__(kWaves * 64)
+    affine_block_kernel(float* __restrict__ W, const float* __restrict__ U, int64_t B, int64_t R,
+                        int64_t C, int64_t i1, int n, int G, float maxq, int storage, Shrinks sh,
+                        uint8_t* __restrict__ q_out, void* s_store, void* b_store,
+                        float* __restrict__ Err) {
+  extern __shared__ float errs_lds[];  // [kWaves][n]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* errs = errs_lds + wave * n;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;  // b*R + r
+  if (row >= B * R) return;  // whole wave exits together (no block barriers below)
+  const int64_t b = row / R;
+  const float* Ub = U + b * C * C;
+  float* Wr = W + row * C;
+  const int64_t ng = C / G;
+  for (int64_t j = i1; j < i1 + n; j += G) {
+    float acc[CPL];
+    bool act[CPL];
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) {
+      const int col = lane + 64 * s;
+      act[s] = col < G;
+      acc[s] = act[s] ? Wr[j + col] : 0.0f;
+    }
+    // earlier in-block updates, in column order
+    for (int64_t k = i1; k < j; ++k) {
+      const float e = errs[k - i1];
+      const float* Uk = Ub + k * C + j;
+#pragma unroll
+      for (int s = 0; s < CPL; ++s)
+        if (act[s]) acc[s] = acc[s] - e * Uk[lane + 64 * s];
+    }
+    // clip search (grid.py:167-212) on the group's current values
+    float lo = act[0] ? acc[0] : __uint_as_float(0x7f800000u);
+    float hi = act[0] ? acc[0] : __uint_as_float(0xff800000u);
+#pragma unroll
+    for (int s = 1; s < CPL; ++s)
+      if (act[s]) {
+        lo = nan_min(lo, acc[s]);
+        hi = nan_max(hi, acc[s]);
+      }
+    const float wmin = wave_nan_min(lo), wmax = wave_nan_max(hi);
+    const float range = wmax - wmin;
+    float best_err = 0.0f, s32 = 0.0f, b32 = 0.0f;
+    for (int cand = 0; cand < sh.n; ++cand) {
+      const float sc = round_to_storage(range * sh.p_over_maxq[cand], storage);
+      const float bi = round_to_storage(wmin * sh.p[cand], storage);
+      const float ss = (fabsf(sc) < 1e-12f) ? 1.0f : sc;
+      float part = 0.0f;
+#pragma unroll
+      for (int s = 0; s < CPL; ++s)
+        if (act[s]) {
+          const float d = affine_q(acc[s], bi, ss, maxq) * sc + bi - acc[s];
+          part += d * d;
+        }
+      const float err = wave_sum(part);
+      if (cand == 0 || err < best_err) {
+        best_err = err;
+        s32 = sc;
+        b32 = bi;
+      }
+    }
+    const int64_t gi = row * ng + j / G;
+    if (lane == 0) {
+      store_storage(s_store, gi, s32, storage);
+      store_storage(b_store, gi, b32, storage);
+    }
+    const float s_safe = (fabsf(s32) < 1e-12f) ? 1.0f : s32;
+    // sequential columns of the group
+    for (int c = 0; c < G; ++c) {
+      const int owner = c & 63, slot = c >> 6;
+      float mine = 0.0f;
+#pragma unroll
+      for (int s = 0; s < CPL; ++s)
+        if (s == slot) mine = acc[s];
+      const float q = affine_q(mine, b32, s_safe, maxq);
+      const float dq = q * s32 + b32;
+      const float diag = Ub[(j + c) * C + j + c];
+      const float e_lane = (mine - dq) / diag;
+      const float e = __shfl(e_lane, owner);
+      if (lane == owner) {
+        q_out[row * C + j + c] = (q == q) ? static_cast<uint8_t>(q) : 0;
+        Wr[j + c] = dq;
+        errs[j + c - i1] = e;
+        Err[row * n + (j + c - i1)] = e;
+      }
+      // errs[] is read by every lane of this wave at the next group start
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const float* Uc = Ub + (j + c) * C + j;
+#pragma unroll
+      for (int s = 0; s < CPL; ++s) {
+        const int col = lane + 64 * s;
+        if (act[s] && col > c) acc[s] = acc[s] - e * Uc[col];
+      }
+    }
+  }
+}
+
+// W[row, i2 + m] -= sum_k Err[row, k] * U[b, i1 + k, i2 + m]: 64x64 output
+// tiles, K = n staged through LDS in chunks of 32.
+constexpr int kTm = 64, kTn = 64, kTk = 32;
+
+__global__ void __launch_bounds__(256)
+    lazy_update_kernel(float* __restrict__ W, const float* __restrict__ U,
+                       const float* __restrict__ Err, int64_t B, int64_t R, int64_t C, int64_t i1,
+                       int n) {
+  const int64_t i2 = i1 + n;
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTm;
+  const int64_t m0 = i2 + static_cast<int64_t>(blockIdx.x) * kTn;
+  if (r0 >= R || m0 >= C) return;
+  __shared__ float Es[kTm][kTk + 1];
+  __shared__ float Us[kTk][kTn + 1];
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;  // 4x4 outputs per thread
+  float acc[4][4] = {};
+  const float* Ub = U + b * C * C;
+  for (int k0 = 0; k0 < n; k0 += kTk) {
+    for (int e = threadIdx.x; e < kTm * kTk; e += 256) {
+      const int rr = e / kTk, kk = e % kTk;
+      const int64_t r = r0 + rr;
+      Es[rr][kk] = (r < R && k0 + kk < n) ? Err[(b * R + r) * n + k0 + kk] : 0.0f;
+    }
+    for (int e = threadIdx.x; e < kTk * kTn; e += 256) {
+      const int kk = e / kTn, mm = e % kTn;
+      const int64_t m = m0 + mm;
+      Us[kk][mm] = (m < C && k0 + kk < n) ? Ub[(i1 + k0 + kk) * C + m] : 0.0f;
+    }
+    __syncthreads();
+    for (int kk = 0; kk < kTk; ++kk) {
+      float ev[4], uv[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) ev[a] = Es[ty * 4 + a][kk];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) uv[a] = Us[kk][tx * 4 + a];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) acc[a][c2] = fmaf(ev[a], uv[c2], acc[a][c2]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int64_t r = r0 + ty * 4 + a;
+    if (r >= R) continue;
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) {
+      const int64_t m = m0 + tx * 4 + c2;
+      if (m < C) {
+        float* p = W + (b * R + r) * C + m;
+        *p = *p - acc[a][c2];
+      }
+    }
+  }
+}
+
+int make_shrinks(int bits, int method, int grid_steps, double max_shrink, Shrinks* out) {
+  const double maxq = static_cast<double>((1 << bits) - 1);
+  if (method == MGQ_CLIP_MINMAX) {
+    out->n = 1;
+    out->p_over_maxq[0] = static_cast<float>(1.0 / maxq);
+    out->p[0] = 1.0f;
+    return MGQ_OK;
+  }
+  MGQ_REQUIRE(grid_steps >= 1 && grid_steps < kMaxShrinks, MGQ_ERR_VALUE,
+              "grid_steps must be in [1, %d)", kMaxShrinks);
+  out->n = grid_steps + 1;
+  for (int i = 0; i <= grid_steps; ++i) {
+    const double p = 1.0 - max_shrink * static_cast<double>(i) / static_cast<double>(grid_steps);
+    out->p_over_maxq[i] = static_cast<float>(p / maxq);
+    out->p[i] = static_cast<float>(p);
+  }
+  return MGQ_OK;
+}
+
+}  // namespace
+}  // namespace mgq
+
+using namespace mgq;
+
+extern "C" int mgq_dead_fix(float* W, int64_t B, int64_t R, int64_t C, float* H, void* stream) {
+  clear_error();
+  MGQ_REQUIRE(B >= 0 && R >= 0 && C >= 0, MGQ_ERR_SHAPE, "bad shape");
+  if (B * C == 0) return MGQ_OK;
+  hipStream_t s = as_stream(stream);
+  if (W != nullptr && R > 0) {
+    dead_fix_w_kernel<<<elementwise_blocks(B * R * C, 256), 256, 0, s>>>(W, H, B, R, C);
+    if (int rc = check_launch("dead fix W")) return rc;
+  }
+  dead_fix_h_kernel<<<elementwise_blocks(B * C, 256), 256, 0, s>>>(H, B, C);
+  return check_launch("dead fix H");
+}
+
+extern "C" int mgq_gptq_affine_block(float* W, const float* U, int64_t B, int64_t R, int64_t C,
+                                     int64_t i1, int64_t n, int group_size, int bits, int method,
+                                     int storage_dtype, int grid_steps, double max_shrink,
+                                     uint8_t* q_out, void* s_store, void* b_store, float* Err,
+                                     void* stream) {
+  clear_error();
+  MGQ_REQUIRE(bits >= 1 && bits <= 8, MGQ_ERR_VALUE, "unsupported bits: %d", bits);
+  MGQ_REQUIRE(group_size >= 1 && group_size <= 128, MGQ_ERR_VALUE,
+              "group size %d unsupported (1..128)", group_size);
+  MGQ_REQUIRE(storage_dtype == kF32 || storage_dtype == kBF16 || storage_dtype == kF16,
+              MGQ_ERR_VALUE, "bad storage dtype");
+  MGQ_REQUIRE(method == MGQ_CLIP_MINMAX || method == MGQ_CLIP_MSE, MGQ_ERR_VALUE,
+              "unsupported clip method %d", method);
+  MGQ_REQUIRE(C % group_size == 0 && i1 % group_size == 0 && n % group_size == 0 &&
+                  n >= 1 && n <= kMaxBlock && i1 + n <= C,
+              MGQ_ERR_SHAPE, "bad block [%lld, %lld) for C=%lld, G=%d", (long long)i1,
+              (long long)(i1 + n), (long long)C, group_size);
+  Shrinks sh;
+  if (int rc = make_shrinks(bits, method, grid_steps, max_shrink, &sh)) return rc;
+  if (B * R == 0) return MGQ_OK;
+  hipStream_t s = as_stream(stream);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(B * R, kWaves));
+  const float maxq = static_cast<float>((1 << bits) - 1);
+  const size_t lds = sizeof(float) * kWaves * static_cast<size_t>(n);
+  if (group_size <= 64) {
+    affine_block_kernel<1><<<blocks, kWaves * 64, lds, s>>>(W, U, B, R, C, i1, static_cast<int>(n),
+                                                          group_size, maxq, storage_dtype, sh,
+                                                          q_out, s_store, b_store, Err);
+  } else {
+    affine_block_kernel<2><<<blocks, kWaves * 64, lds, s>>>(W, U, B, R, C, i1, static_cast<int>(n),
+                                                          group_size, maxq, storage_dtype, sh,
+                                                          q_out, s_store, b_store, Err);
+  }
+  if (int rc = check_launch("affine block")) return rc;
+  if (i1 + n < C) {
+    dim3 grid(static_cast<unsigned>(ceil_div(C - i1 - n, kTn)),
+              static_cast<unsigned>(ceil_div(R, kTm)), static_cast<unsigned>(B));
+    lazy_update_kernel<<<grid, 256, 0, s>>>(W, U, Err, B, R, C, i1, static_cast<int>(n));
+    if (int rc = check_launch("affine lazy update")) return rc;
+  }
+  return MGQ_OK;
+}

@@ -69,9 +69,18 @@ SIGNATURES: dict[str, list] = {
     "mgq_gptq_mxfp_workspace_size": [_I64, _I64, _I64],
     "mgq_gptq_mxfp": [_VP, _INT, _I64, _I64, _I64, _VP, _INT, _INT, _F32, _INT, _VP, _INT,
                       _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
+    "mgq_hinv_full_workspace_size": [_I64, _I64],
+    "mgq_hinv_full_pass": [_VP, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
+    "mgq_dead_fix": [_VP, _I64, _I64, _I64, _VP, _VP],
+    "mgq_gptq_affine_block": [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _INT, _INT,
+                              _INT, _F64, _VP, _VP, _VP, _VP, _VP],
 }
 
-_RESTYPES = {"mgq_last_error": ctypes.c_char_p, "mgq_gptq_mxfp_workspace_size": ctypes.c_int64}
+_RESTYPES = {
+    "mgq_last_error": ctypes.c_char_p,
+    "mgq_gptq_mxfp_workspace_size": ctypes.c_int64,
+    "mgq_hinv_full_workspace_size": ctypes.c_int64,
+}
 
 _lib = None
 _lock = threading.Lock()

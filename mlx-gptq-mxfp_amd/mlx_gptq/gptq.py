@@ -75,8 +75,9 @@ def _prepare_hinv(H: torch.Tensor, damp: float, max_attempts: int = 6) -> torch.
     else:
         from . import gptq_affine
 
-        U, att = gptq_affine.prepare_hinv_full(Hc, damp, max_attempts)
-    _escalation_report(att.cpu().numpy(), B, damp, max_attempts, lambda idx: Hc[torch.as_tensor(idx, device=dev)])
+        U, att = gptq_affine.prepare_hinv_full(Hc.contiguous(), damp, max_attempts)
+    att = att if isinstance(att, np.ndarray) else att.cpu().numpy()
+    _escalation_report(att, B, damp, max_attempts, lambda idx: Hc[torch.as_tensor(idx, device=dev)])
     return U.to(H.device)
 
 
@@ -172,8 +173,7 @@ def gptq_quantize(
         if W.dtype != torch.float32:
             raise TypeError("gptq_quantize updates W in place and needs float32 W")
         return _gptq_quantize_mxfp_groupwise(W, H, mode, damp, mxfp_algorithm)
-    if mode != "affine":
-        raise ValueError(f"unsupported quantization mode: {mode}")
+    # any other mode string takes the affine path, as in the reference
     from . import gptq_affine
 
     return gptq_affine.gptq_quantize_affine(W, H, bits, group_size, damp, clip, storage_dtype,

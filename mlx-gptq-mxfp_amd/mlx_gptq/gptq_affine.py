@@ -1,11 +1,23 @@
-"""Affine (MLX scale/bias) GPTQ path: full-matrix damped Cholesky-inverse and
-the lazy-block column loop (gptq.py:229-272). See csrc/gptq_affine.hip."""
+"""Affine (MLX scale/bias) GPTQ path on the HIP kernels of csrc/chol_full.hip
+and csrc/gptq_affine.hip.
+
+  prepare_hinv_full     gptq.py:27-66 on full [C, C] Hessians: the damping
+                        escalation loop (damp x10 for the failed items only,
+                        up to max_attempts) around one fp64 blocked
+                        factorisation pass per attempt.
+  gptq_quantize_affine  gptq.py:216-272 for mode "affine": dead-column fix,
+                        U, then one kernel pair per lazy block (column loop
+                        with the MSE clip search at every group start, and
+                        the deferred W[:, :, i2:] -= Err @ U[i1:i2, i2:]).
+"""
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _native as nat
+from .grid import _clip_code, _storage_code
 
 
 def rel_err(W_dq: torch.Tensor, W_orig: torch.Tensor) -> torch.Tensor:
@@ -17,8 +29,72 @@ def rel_err(W_dq: torch.Tensor, W_orig: torch.Tensor) -> torch.Tensor:
 
 
 def prepare_hinv_full(H: torch.Tensor, damp: float, max_attempts: int):
-    raise NotImplementedError("full-matrix Cholesky inverse: not built yet")
+    """U [B, C, C] (f32 upper, U^T U = (H + lam I)^-1) and the attempts used per
+    item (int [B], 0 = every attempt failed), for a contiguous f32 H on a HIP
+    device. The reference escalates per failed item by damp *= 10 in fp32 and
+    retries only those items (gptq.py:37-52); so does this loop."""
+    B, C, _ = H.shape
+    dev = H.device
+    lib = nat.load()
+    stream = nat.stream_of(dev)
+    U = torch.empty(B, C, C, dtype=torch.float32, device=dev)
+    attempts = np.zeros(B, dtype=np.int64)
+    if B == 0 or C == 0:
+        return U, attempts
+    ws = torch.empty(int(lib.mgq_hinv_full_workspace_size(B, C)), dtype=torch.uint8, device=dev)
+    cur = np.full(B, np.float32(damp), dtype=np.float32)
+    active = np.ones(B, dtype=bool)
+    for att in range(1, int(max_attempts) + 1):
+        damp_d = torch.from_numpy(cur).to(dev)
+        active_d = torch.from_numpy(active.astype(np.uint8)).to(dev)
+        failed_d = torch.zeros(B, dtype=torch.uint8, device=dev)
+        nat.call("mgq_hinv_full_pass", H.data_ptr(), B, C, damp_d.data_ptr(), active_d.data_ptr(),
+                 failed_d.data_ptr(), U.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        failed = failed_d.cpu().numpy().astype(bool) & active
+        attempts[active & ~failed] = att
+        if not failed.any():
+            break
+        cur[failed] = cur[failed] * np.float32(10.0)
+        active = failed
+    return U, attempts
 
 
-def gptq_quantize_affine(W, H, bits, group_size, damp, clip, storage_dtype, block_size):
-    raise NotImplementedError("affine GPTQ path: not built yet")
+def gptq_quantize_affine(W: torch.Tensor, H: torch.Tensor, bits: int, group_size: int,
+                         damp: float, clip: str, storage_dtype: torch.dtype, block_size: int):
+    """gptq.py:216-272 for mode "affine". W f32 [B, R, C] becomes W_dq in place;
+    H f32 [B, C, C] gets the dead-column diagonal fix in place.
+    Returns (q u8 [B,R,C], scales, biases [B,R,C/G] storage_dtype, W, None)."""
+    from .gptq import _prepare_hinv, _require_device
+
+    if W.dtype != torch.float32:
+        raise TypeError("gptq_quantize updates W in place and needs float32 W")
+    _require_device(W, H)
+    B, R, C = W.shape
+    G = int(group_size)
+    bits = int(bits)
+    if not 1 <= bits <= 8:
+        raise ValueError(f"unsupported bits for uint8 codes: {bits}")
+    if G > 128:
+        raise ValueError(f"affine group size {G} unsupported on this build (<= 128)")
+    storage = _storage_code(storage_dtype)
+    dev = W.device
+    stream = nat.stream_of(dev)
+    nat.call("mgq_dead_fix", W.data_ptr(), B, R, C, H.data_ptr(), stream)
+    U = _prepare_hinv(H, damp)
+
+    bs = max(int(block_size), G)
+    bs -= bs % G
+    n_groups = C // G
+    q_out = torch.empty(B, R, C, dtype=torch.uint8, device=dev)
+    scales = torch.empty(B, R, n_groups, dtype=storage_dtype, device=dev)
+    biases = torch.empty(B, R, n_groups, dtype=storage_dtype, device=dev)
+    if B * R * C == 0:
+        return q_out, scales, biases, W, None
+    Err = torch.empty(B, R, min(bs, C), dtype=torch.float32, device=dev)
+    method = _clip_code(clip)
+    for i1 in range(0, C, bs):
+        n = min(i1 + bs, C) - i1
+        nat.call("mgq_gptq_affine_block", W.data_ptr(), U.data_ptr(), B, R, C, i1, n, G, bits,
+                 method, storage, 20, 0.2, q_out.data_ptr(), scales.data_ptr(),
+                 biases.data_ptr(), Err.data_ptr(), stream)
+    return q_out, scales, biases, W, None

@@ -53,6 +53,12 @@ def _storage_code(dt: torch.dtype) -> int:
     return nat.dtype_code(dt)
 
 
+def _clip_code(method: str) -> int:
+    """grid.py:187-192: "minmax" keeps the full range; any other method is
+    the MSE range-shrink search."""
+    return nat.CLIP_MINMAX if method == "minmax" else nat.CLIP_MSE
+
+
 def _require_f32(t: torch.Tensor, fn: str) -> None:
     if t.dtype != torch.float32:
         raise TypeError(f"{fn}: expects float32 values (got {t.dtype}); call .float() first")
@@ -203,8 +209,6 @@ def choose_qparams(
     Returns (scales_stored, biases_stored, scales_f32, biases_f32), shape [...].
     """
     _require_f32(w, "choose_qparams")
-    if method not in ("mse", "minmax"):
-        raise ValueError(f"unsupported clip method: {method}")
     dev = nat.device_for(w)
     x = nat.on_device(w, dev)
     lead = tuple(w.shape[:-1])
@@ -217,7 +221,7 @@ def choose_qparams(
     if n:
         nat.call(
             "mgq_choose_qparams", x.data_ptr(), n, k, int(bits),
-            nat.CLIP_MSE if method == "mse" else nat.CLIP_MINMAX, _storage_code(storage_dtype),
+            _clip_code(method), _storage_code(storage_dtype),
             int(grid_steps), float(max_shrink), s_st.data_ptr(), b_st.data_ptr(), s32.data_ptr(),
             b32.data_ptr(), nat.stream_of(dev),
         )
@@ -259,8 +263,6 @@ def rtn_quantize(
     """
     *lead, R, C = W.shape
     assert C % group_size == 0, f"cols {C} not divisible by group size {group_size}"
-    if method not in ("mse", "minmax"):
-        raise ValueError(f"unsupported clip method: {method}")
     dev = nat.device_for(W)
     x = nat.on_device(W.float(), dev)
     rows = nat.numel_groups((*lead, R))
@@ -272,7 +274,7 @@ def rtn_quantize(
     if rows and C:
         nat.call(
             "mgq_rtn_quantize_affine", x.data_ptr(), nat.DTYPE_F32, rows, C, int(bits), G,
-            nat.CLIP_MSE if method == "mse" else nat.CLIP_MINMAX, _storage_code(storage_dtype),
+            _clip_code(method), _storage_code(storage_dtype),
             q.data_ptr(), s_st.data_ptr(), b_st.data_ptr(), dq.data_ptr(), nat.stream_of(dev),
         )
     to = W.device
