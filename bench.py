@@ -41,16 +41,26 @@ def _args(argv=None):
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of the CPU-oracle sample (0 disables it)")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="before the steps, run one plain elementwise copy (torch.neg) of this many "
+                         "MiB: the reference dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                         "to bytes")
     return ap.parse_args(argv)
 
 
 def _hessian_traffic():
-    """HBM bytes per Hessian launch measured with rocprofv3 FETCH_SIZE /
-    WRITE_SIZE, if the profile summary is present (profiles/)."""
-    p = os.path.join(ROOT, "profiles", "hessian_moe_cfg4_traffic.json")
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f).get("bytes_per_launch")
+    """HBM bytes per gate_up Hessian launch (routed-gather SYRK kernel):
+    rocprofv3 FETCH_SIZE + WRITE_SIZE of that dispatch, each scaled by what
+    the counter reads for a plain 1 GiB copy, as committed under profiles/
+    (the profiler cannot run inside this process). None if absent."""
+    p = os.path.join(ROOT, "profiles", "bench_moe_cfg4_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        per = json.load(f).get("bytes_per_dispatch", {})
+    for k, v in per.items():
+        if k.startswith("mgq::syrk_tile_kernel<true>"):
+            return round(float(v))
     return None
 
 
@@ -100,6 +110,15 @@ def main(argv=None) -> int:
         evs[5].record()
         return q_gu, s_gu, q_dn, s_dn, packed
 
+    if args.copy_calib_mib > 0:
+        n = args.copy_calib_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)  # reads and writes exactly n*4 bytes
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -144,7 +163,7 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16-mfma+fp32",
+        "dtype": "bf16+fp32",
         "data": "synthetic (seeded hidden states, router, expert weights)",
         "config": {
             "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
