@@ -10,13 +10,11 @@
 //
 // Tile kernel (256 threads = 4 waves, 1 workgroup per CU):
 //   - output tile 256x256, each wave 128x128 = 4x4 blocks of
-//     v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane);
-//   - K stages of 64 tokens, double-buffered in LDS (2 x 64 KB); a thread
-//     loads an 8-token x 8-channel block with 16-byte global loads
-//     (coalesced along channels), transposes it in registers with v_perm so
-//     channel rows become token-contiguous, and stores 16-byte rows into an
-//     XOR-swizzled LDS layout that keeps both the stores and the MFMA operand
-//     reads (ds_read_b128) free of bank conflicts;
+//     v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, in AGPRs);
+//   - token rows are copied HBM -> LDS by global_load_lds_dwordx4 with a
+//     scalar (SGPR) row address per token, so the gather costs no vector
+//     work; MFMA operands are read with ds_read_b64_tr_b16 transposing loads
+//     from the token-major LDS rows (see syrk_dma_kernel);
 //   - one work item accumulates at most 262144 tokens in the MFMA fp32
 //     accumulators (longer token ranges are split into partial tiles), which
 //     bounds the accumulation chain well inside the 1e-5 Frobenius budget.
@@ -39,12 +37,9 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-// Native clang vectors (not HIP's u32x4 struct) so register arrays of them
-// are promoted to VGPRs instead of private memory.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;
-constexpr int kKs = 64;          // tokens per LDS stage
+constexpr int kKs = 64;          // token granularity of work-item ranges
 constexpr int kThreads = 256;
 constexpr int64_t kMaxItemTokens = 262144;  // longest fp32 accumulation chain per item
 constexpr int kXcds = 8;
@@ -76,76 +71,8 @@ struct PlanHeader {
 
 constexpr int64_t kAlign = 256;
 inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
-
-// LDS: [buf][operand][256 rows][8 chunks of 16 B], chunk index XOR-swizzled.
-__device__ inline int swz(int row, int chunk) {
-  return row * 8 + (chunk ^ ((row ^ (row >> 3)) & 7));
-}
-
-__device__ inline uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
-}
-
-// Per-stage global traffic of a loader thread: its 8 tokens' rows (one
-// 16-byte load per token and operand). The three steps are kept apart so the
-// loop can software-pipeline them: gather indices for stage s+2 and row
-// loads for stage s+1 are in flight while stage s runs on the MFMAs; the
-// zero-masking of out-of-range tokens happens only when the rows are stored
-// to LDS. Everything is branch-free (a branch around a load makes the
-// compiler wait for it at the join). Out-of-range tokens read a clamped
-// valid row; gathered indices are clamped into X so a bad index cannot
-// fault.
-template <bool GATHER>
-__device__ inline void load_index(const int32_t* __restrict__ row_index, int64_t tok0,
-                                  int64_t t_end, int32_t (&idx)[8]) {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int64_t t = tok0 + r;
-    idx[r] = GATHER ? row_index[t < t_end ? t : t_end - 1] : 0;
-  }
-}
-
-template <bool GATHER>
-__device__ inline void load_rows(const uint16_t* __restrict__ X, int64_t ldx, int64_t n_rows,
-                                 const int32_t (&idx)[8], int64_t tok0, int64_t t_end,
-                                 int64_t chanA, int64_t chanB, u32x4 (&ra)[8], u32x4 (&rb)[8]) {
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int64_t t = tok0 + r;
-    const int64_t row = GATHER ? min(max(static_cast<int64_t>(idx[r]), int64_t(0)), n_rows - 1)
-                               : (t < t_end ? t : t_end - 1);
-    const uint16_t* p = X + row * ldx;
-    ra[r] = *reinterpret_cast<const u32x4*>(p + chanA);
-    rb[r] = *reinterpret_cast<const u32x4*>(p + chanB);
-  }
-}
-
-__device__ inline void mask_rows(int64_t tok0, int64_t t_end, bool ok, u32x4 (&rr)[8]) {
-  const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int r = 0; r < 8; ++r) rr[r] = (ok && tok0 + r < t_end) ? rr[r] : z;
-}
-
-// Transpose an 8x8 bf16 block in registers (v_perm) so each channel's 8
-// tokens are contiguous, and store the 8 channel rows into the swizzled LDS
-// tile. Row cb*8+c, chunk kb lands at (cb*8+c)*8 + (kb ^ f(row)) with
-// f(row) = (c ^ cb) & 7, i.e. chunk (u ^ c) for u = (kb ^ cb) & 7.
-__device__ inline uint32_t dword(const u32x4& v, int d) { return v[d]; }
-
-__device__ inline void store_block(u32x4* __restrict__ lds, int cb, int u, const u32x4 (&in)[8]) {
-  u32x4* base = lds + cb * 64;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-    const int d = c >> 1;  // dword holding channel c of each token
-    u32x4 o;
-    o.x = perm(dword(in[1], d), dword(in[0], d), sel);
-    o.y = perm(dword(in[3], d), dword(in[2], d), sel);
-    o.z = perm(dword(in[5], d), dword(in[4], d), sel);
-    o.w = perm(dword(in[7], d), dword(in[6], d), sel);
-    base[c * 8 + (u ^ c)] = o;
-  }
-}
+// A row of C bf16 zeros that tail tokens (past a work item's range) load.
+inline int64_t zero_row_bytes(int64_t C) { return align_up(2 * C); }
 
 // Flush the wave's 128x128 accumulators into `out` (row stride ld). Direct
 // tiles (H_g, global coordinates) keep the lower triangle and
@@ -155,11 +82,38 @@ __device__ inline void store_block(u32x4* __restrict__ lds, int cb, int u, const
 // scalar registers.
 __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uint32_t ld_s,
                              bool direct, bool add, uint32_t C, uint32_t gi0, uint32_t gj0,
-                             int lane) {
+                             int lane, bool interior) {
   uint32_t ld;
   asm volatile("v_mov_b32 %0, %1" : "=v"(ld) : "s"(ld_s));
   const uint32_t gj_l = gj0 + (lane & 31);
   const uint32_t gi_l = gi0 + 4 * (lane >> 5);
+  if (interior) {
+    // Strictly-lower tile inside H: no masking. Registers 4q..4q+3 of a
+    // block hold rows gi..gi+3 of one column gj, so the mirrored values are
+    // 4 consecutive floats of row gj: one 16-byte store.
+#pragma unroll
+    for (int ma = 0; ma < 4; ++ma) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const uint32_t gi = gi_l + ma * 32 + 8 * rq;
+#pragma unroll
+        for (int na = 0; na < 4; ++na) {
+          const uint32_t gj = gj_l + na * 32;
+          float nv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float* p = out + ((gi + e) * ld + gj);
+            const float v = acc[ma][na][4 * rq + e];
+            nv[e] = add ? (*p + v) : v;
+            *p = nv[e];
+          }
+          const float4 m = {nv[0], nv[1], nv[2], nv[3]};
+          *reinterpret_cast<float4*>(out + (gj * ld + gi)) = m;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ma = 0; ma < 4; ++ma) {
 #pragma unroll
@@ -186,18 +140,123 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS SYRK (production kernel).
+//
+// Token rows go from HBM straight into LDS with global_load_lds_dwordx4 (no
+// VGPR staging, no register transpose): one instruction moves one token's
+// 256 A channels (lanes 0-31) and 256 B channels (lanes 32-63), 1 KB, with
+// a 64-bit SGPR row address, so the routed gather costs scalar work only.
+// LDS keeps token-major rows (as in HBM); MFMA operands (one channel x 8
+// consecutive tokens per lane) come out of ds_read_b64_tr_b16, which hands
+// lane i of each 16-lane group element i%4 of source lanes 4j + i/4, j=0..3:
+// pointing source lane 4j+q at token j, channels 4q..4q+3 gives lane i
+// channel i of tokens 0..3. Four 32-token stages are in flight; each wave
+// waits for its own DMA of a stage (vmcnt) before the stage barrier. The
+// 16-byte chunk index of LDS token row t is XORed with 4*(t & 3), so the 64
+// bytes a transposed read takes from each of its 8 token rows land on four
+// distinct 64-byte bank groups (two LDS cycles per read, no conflicts).
+constexpr int kTokB = 1024;  // LDS bytes per token: A row | B row
+#ifndef MGQ_SYRK_KB
+#define MGQ_SYRK_KB 64  // tokens per LDS stage (one barrier each)
+#endif
+#ifndef MGQ_SYRK_NB
+#define MGQ_SYRK_NB 2   // stage buffers (NB - 1 stages of DMA in flight)
+#endif
+constexpr int kDK = MGQ_SYRK_KB;
+constexpr int kDBuf = MGQ_SYRK_NB;
+constexpr int kStageB = kDK * kTokB;
+constexpr int kDmaWave = kDK / 4;  // tokens (= DMA instructions) per wave and stage
+static_assert(kDBuf * kStageB <= 160 * 1024, "LDS budget");
+static_assert((kDBuf - 2) * kDmaWave <= 63, "vmcnt range");
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+__device__ inline void dma_row(uint32_t lds_dst, uint32_t voff, const void* saddr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_dst), "v"(voff), "s"(saddr)
+               : "memory");
+}
+
+// Wait until at most N of this wave's DMA loads are outstanding and its LDS
+// reads / scalar loads are done, then barrier.
+template <int N>
+__device__ inline void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "i"(N) : "memory");
+}
+
+// `ahead` stages of DMA (kDmaWave loads each) were issued after the stage
+// being waited for; the count is an immediate, so dispatch on it.
+__device__ inline void stage_barrier_ahead(int ahead) {
+  if constexpr (kDBuf - 2 >= 3) {
+    if (ahead >= 3) {
+      stage_barrier<3 * kDmaWave>();
+      return;
+    }
+  }
+  if constexpr (kDBuf - 2 >= 2) {
+    if (ahead >= 2) {
+      stage_barrier<2 * kDmaWave>();
+      return;
+    }
+  }
+  if constexpr (kDBuf - 2 >= 1) {
+    if (ahead >= 1) {
+      stage_barrier<kDmaWave>();
+      return;
+    }
+  }
+  stage_barrier<0>();
+}
+
+__device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + 4 * kTokB));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+template <bool GATHER>
+__device__ inline void stage_rows(const char* __restrict__ Xb, uint32_t ldx2, uint32_t n_rows,
+                                  const int32_t* __restrict__ row_index, int64_t t0, int64_t k1,
+                                  const char* zero_row, const char* (&src)[kDmaWave]) {
+#pragma unroll
+  for (int i = 0; i < kDmaWave; ++i) {
+    const int64_t t = t0 + i;
+    uint32_t row;
+    if (GATHER) {
+      const uint32_t r = static_cast<uint32_t>(row_index[t < k1 ? t : k1 - 1]);
+      row = r < n_rows ? r : n_rows - 1;
+    } else {
+      row = static_cast<uint32_t>(t < k1 ? t : k1 - 1);
+    }
+    src[i] = t < k1 ? Xb + static_cast<uint64_t>(row) * ldx2 : zero_row;
+  }
+}
+
+__device__ inline void issue_stage(uint32_t dst, const uint32_t (&voff)[4],
+                                   const char* const (&src)[kDmaWave]) {
+#pragma unroll
+  for (int i = 0; i < kDmaWave; ++i) dma_row(dst + i * kTokB, voff[i & 3], src[i]);
+}
+
 template <bool GATHER>
 __global__ void __launch_bounds__(kThreads, 1)
-    syrk_tile_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
-                     const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
-                     float* __restrict__ H, float* __restrict__ partials, int accumulate) {
-  __shared__ u32x4 lds[2][2][kTile * 8];  // 2 bufs x (A, B) x 256 rows x 128 B = 128 KB
+    syrk_dma_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
+                    const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
+                    float* __restrict__ H, float* __restrict__ partials, int accumulate,
+                    const uint16_t* __restrict__ zero_row) {
+  __shared__ __attribute__((aligned(1024))) char lds[kDBuf * kStageB];
 
   const HessItem it = items[blockIdx.x];
   if (it.g < 0) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 1, wc = wave & 1;
   const bool diag = it.ti == it.tj;
   const bool direct = it.slot < 0;
@@ -207,24 +266,32 @@ __global__ void __launch_bounds__(kThreads, 1)
   const uint32_t gi0 = (direct ? static_cast<uint32_t>(it.ti) * kTile : 0u) + wr * 128;
   const uint32_t gj0 = (direct ? static_cast<uint32_t>(it.tj) * kTile : 0u) + wc * 128;
 
-  // loader role: 8-token block kb, 8-channel block cb, for A and (off-diagonal) B
-  const int kb = tid & 7, cb = tid >> 3;
-  const int u = (kb ^ cb) & 7;
-  const int64_t cA = static_cast<int64_t>(it.ti) * kTile + cb * 8;
-  const int64_t cB = static_cast<int64_t>(it.tj) * kTile + cb * 8;
-  const bool okA = cA < C, okB = cB < C;
-  const int64_t chanA = okA ? cA : 0;
-  const int64_t chanB = diag ? chanA : (okB ? cB : 0);
-
-  // MFMA operand offsets (u32x4 units) within a 256-row LDS tile: row
-  // base + 32m + l, chunk 2ks + h lands at row*8 + ((2ks + h) ^ f(row)) with
-  // f(row) = (l ^ (l >> 3) ^ 4(m & 1)) & 7, so only xo[ks ^ 2(m & 1)] varies.
-  const int l = lane & 31, h = lane >> 5;
-  const int v = h ^ ((l ^ (l >> 3)) & 7);
-  int xo[4];
+  // DMA lane role: slot (lane & 31) of the A (lane < 32) or B half of LDS
+  // token row t holds chunk slot ^ 4*(t & 3); channels past C are clamped (they
+  // only feed output rows / columns >= C, which are never stored). Diagonal
+  // tiles load the A channels into both halves.
+  const int half = lane >> 5;
+  const int64_t tile_ch = static_cast<int64_t>(half && !diag ? it.tj : it.ti) * kTile;
+  uint32_t voff[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) xo[c] = l * 8 + (v ^ (2 * c));
-  const int a_base = wr * 128 * 8, b_base = wc * 128 * 8;
+  for (int f = 0; f < 4; ++f) {
+    const int64_t ch = tile_ch + 8 * ((lane & 31) ^ (4 * f));
+    voff[f] = static_cast<uint32_t>(2 * (ch < C - 8 ? ch : C - 8));
+  }
+  // Transposed-read lane role: group g = lane/16, source j = (lane/4)%4, q = lane%4.
+  // Source j reads LDS token row 4r + j (+ 8, 16 multiples), so its swizzle is j.
+  const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+  const uint32_t rd_lo = static_cast<uint32_t>((8 * (g >> 1) + j) * kTokB + (g & 1) * 32 +
+                                               (q >> 1) * 16 + (q & 1) * 8);
+  uint32_t offA[4], offB[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    offA[m] = rd_lo + wr * 256 + (m ^ j) * 64;
+    offB[m] = rd_lo + 512 + wc * 256 + (m ^ j) * 64;
+  }
+  const lds_char_t* lds3 = (const lds_char_t*)lds;
+  const uint32_t lds_u32 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds3));
+  const uint32_t wave_dst = wave * kDmaWave * kTokB;
 
   f32x16_t acc[4][4];
 #pragma unroll
@@ -234,57 +301,77 @@ __global__ void __launch_bounds__(kThreads, 1)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[ma][na][r] = 0.0f;
 
-  u32x4 ra[8], rb[8];
-  int32_t idx[8];
+  const char* Xb = reinterpret_cast<const char*>(X);
+  const char* zr = reinterpret_cast<const char*>(zero_row);
+  const uint32_t ldx2 = static_cast<uint32_t>(2 * ldx);
+  const uint32_t nr = static_cast<uint32_t>(n_rows);
   const int64_t k0 = it.k0, k1 = it.k1;
-  const int n_stages = static_cast<int>((k1 - k0 + kKs - 1) / kKs);
-  const int64_t tk = k0 + kb * 8;  // this thread's first token of stage 0
-  if (n_stages > 0) {
-    load_index<GATHER>(row_index, tk, k1, idx);
-    load_rows<GATHER>(X, ldx, n_rows, idx, tk, k1, chanA, chanB, ra, rb);
-    if (n_stages > 1) load_index<GATHER>(row_index, tk + kKs, k1, idx);
-    mask_rows(tk, k1, okA, ra);
-    mask_rows(tk, k1, okB, rb);
-    store_block(lds[0][0], cb, u, ra);
-    if (!diag) store_block(lds[0][1], cb, u, rb);
-  }
-  __syncthreads();
-  for (int s = 0; s < n_stages; ++s) {
-    const int buf = s & 1;
-    const bool more = s + 1 < n_stages;
-    const int64_t t1 = tk + static_cast<int64_t>(s + 1) * kKs;  // stage s+1
-    if (more) {
-      load_rows<GATHER>(X, ldx, n_rows, idx, t1, k1, chanA, chanB, ra, rb);
-      if (s + 2 < n_stages) load_index<GATHER>(row_index, t1 + kKs, k1, idx);
+  const int n_stages = static_cast<int>((k1 - k0 + kDK - 1) / kDK);
+  const int64_t twave = k0 + wave * kDmaWave;  // this wave's first token of stage 0
+
+  const char* src[kDmaWave];
+  // prologue: stages 0 .. kDBuf-2 in flight
+#pragma unroll
+  for (int p = 0; p < kDBuf - 1; ++p) {
+    if (p < n_stages) {
+      stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + p * kDK, k1, zr, src);
+      issue_stage(lds_u32 + p * kStageB + wave_dst, voff, src);
     }
-    const u32x4* A = lds[buf][0] + a_base;
-    const u32x4* B = (diag ? lds[buf][0] : lds[buf][1]) + b_base;
+  }
+  if (kDBuf - 1 < n_stages)
+    stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + (kDBuf - 1) * kDK, k1, zr, src);
+
+  int rbuf = 0, wbuf = kDBuf - 1;  // buffer of stage s, buffer of stage s + kDBuf - 1
+  for (int s = 0; s < n_stages; ++s) {
+    stage_barrier_ahead(n_stages - 1 - s);
+    const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
+    bf16x8_t fa[2][4], fb[2][4];
 #pragma unroll
-    for (int ks = 0; ks < kKs / 16; ++ks) {
-      bf16x8_t af[4], bfv[4];
+    for (int m = 0; m < 4; ++m) {
+      fa[0][m] = tr_frag(lds3 + rd + offA[m]);
+      fb[0][m] = tr_frag(lds3 + rd + offB[m]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int off = m * 256 + xo[ks ^ (2 * (m & 1))];
-        af[m] = __builtin_bit_cast(bf16x8_t, A[off]);
-        bfv[m] = __builtin_bit_cast(bf16x8_t, B[off]);
+    for (int ks = 0; ks < kDK / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < kDK / 16) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          fa[cur ^ 1][m] = tr_frag(lds3 + rd + offA[m] + (ks + 1) * 16 * kTokB);
+          fb[cur ^ 1][m] = tr_frag(lds3 + rd + offB[m] + (ks + 1) * 16 * kTokB);
+        }
       }
+      if (ks == 0 && s + kDBuf - 1 < n_stages) {
+        // the buffer of stage s-1: every wave finished it before the barrier
+        issue_stage(lds_u32 + wbuf * kStageB + wave_dst, voff, src);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ma = 0; ma < 4; ++ma)
 #pragma unroll
         for (int na = 0; na < 4; ++na)
-          acc[ma][na] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ma], bfv[na], acc[ma][na], 0, 0, 0);
+          acc[ma][na] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][ma], fb[cur][na],
+                                                                acc[ma][na], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
-      mask_rows(t1, k1, okA, ra);
-      mask_rows(t1, k1, okB, rb);
-      store_block(lds[buf ^ 1][0], cb, u, ra);
-      if (!diag) store_block(lds[buf ^ 1][1], cb, u, rb);
-    }
-    __syncthreads();
+    if (s + kDBuf < n_stages)
+      stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + static_cast<int64_t>(s + kDBuf) * kDK,
+                         k1, zr, src);
+    rbuf = rbuf + 1 == kDBuf ? 0 : rbuf + 1;
+    wbuf = wbuf + 1 == kDBuf ? 0 : wbuf + 1;
   }
   // Empty ranges (n_stages == 0) still flush, so an unrouted group gets H = 0.
-  flush(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane);
+  const bool interior =
+      direct && it.ti > it.tj && (static_cast<int64_t>(it.ti) + 1) * kTile <= C;
+  flush(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
+        interior);
+}
+
+__global__ void zero_fill_kernel(uint32_t* __restrict__ p, int64_t n_words) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_words;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
 }
 
 // Sum the K-split partial tiles of one output tile in slot order and write
@@ -431,7 +518,7 @@ extern "C" int mgq_hessian_plan(int64_t C, int64_t n_groups, const int64_t* offs
   const int64_t need = p.hdr.plan_bytes;
   if (plan_bytes) *plan_bytes = need;
   if (workspace_bytes)
-    *workspace_bytes = need + p.hdr.n_slots * static_cast<int64_t>(kTile) * kTile * 4;
+    *workspace_bytes = need + zero_row_bytes(C) + p.hdr.n_slots * static_cast<int64_t>(kTile) * kTile * 4;
   if (plan == nullptr) return MGQ_OK;  // size query
   MGQ_REQUIRE(plan_capacity >= need, MGQ_ERR_WORKSPACE, "plan buffer %lld < %lld bytes",
               (long long)plan_capacity, (long long)need);
@@ -463,23 +550,27 @@ extern "C" int mgq_hessian(const void* X, int64_t n_rows, int64_t ldx, int64_t C
               (long long)n_rows);
   MGQ_REQUIRE(C <= 46340, MGQ_ERR_SHAPE, "hessian: C=%lld exceeds 46340 (C*C >= 2^31)",
               (long long)C);
-  const int64_t need = h.plan_bytes + h.n_slots * static_cast<int64_t>(kTile) * kTile * 4;
+  const int64_t zbytes = zero_row_bytes(C);
+  const int64_t need = h.plan_bytes + zbytes + h.n_slots * static_cast<int64_t>(kTile) * kTile * 4;
   MGQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, MGQ_ERR_WORKSPACE,
               "hessian workspace %lld < %lld bytes", (long long)workspace_bytes, (long long)need);
   hipStream_t s = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   const HessItem* items = reinterpret_cast<const HessItem*>(ws + h.items_off);
   const SplitTile* split = reinterpret_cast<const SplitTile*>(ws + h.split_off);
-  float* partials = reinterpret_cast<float*>(ws + h.plan_bytes);
+  uint16_t* zero_row = reinterpret_cast<uint16_t*>(ws + h.plan_bytes);
+  float* partials = reinterpret_cast<float*>(ws + h.plan_bytes + zbytes);
   if (h.n_items > 0) {
+    zero_fill_kernel<<<1, 256, 0, s>>>(reinterpret_cast<uint32_t*>(zero_row), zbytes / 4);
+    if (int rc = check_launch("hessian zero row")) return rc;
     if (row_index) {
-      syrk_tile_kernel<true><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
+      syrk_dma_kernel<true><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
           static_cast<const uint16_t*>(X), n_rows, ldx, C, row_index, items, H, partials,
-          accumulate);
+          accumulate, zero_row);
     } else {
-      syrk_tile_kernel<false><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
+      syrk_dma_kernel<false><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
           static_cast<const uint16_t*>(X), n_rows, ldx, C, nullptr, items, H, partials,
-          accumulate);
+          accumulate, zero_row);
     }
     if (int rc = check_launch("hessian syrk")) return rc;
   }
