@@ -59,7 +59,7 @@ def _hessian_traffic():
     with open(p) as f:
         per = json.load(f).get("bytes_per_dispatch", {})
     for k, v in per.items():
-        if k.startswith("mgq::syrk_tile_kernel<true>"):
+        if k.startswith("mgq::syrk_dma_kernel<true>"):
             return round(float(v))
     return None
 
@@ -137,7 +137,7 @@ def main(argv=None) -> int:
     hess_ms = float(phase[0])
     achieved = hess_flops / (hess_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "syrk_tile_kernel (gate_up Hessian, routed gather)",
+        "kernel": "syrk_dma_kernel (gate_up Hessian, routed gather)",
         "bound": "mfma",
         "achieved": round(achieved, 1),
         "peak": PEAK_BF16_TFLOPS,

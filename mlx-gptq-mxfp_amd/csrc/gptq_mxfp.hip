@@ -80,6 +80,14 @@ __device__ inline float quant_fast(float w, float inv_scale, float scale) {
   return MODE == kMxfp4 ? mx4_dq(w, inv_scale, scale) : mx8_dq(w, inv_scale, scale);
 }
 
+// value(code) * scale for code i of a packed group: exactly the dq that
+// quant_exact returned for that code.
+template <int MODE>
+__device__ inline float code_value(const uint32_t (&codes)[kG / 4], int i, float scale) {
+  const uint32_t code = (codes[i / 4] >> (8 * (i % 4))) & 0xffu;
+  return (MODE == kMxfp4 ? e2m1_value(code) : e4m3_value(code)) * scale;
+}
+
 // e^T Hg e with fused multiply-adds in a fixed order. Hg is the block's
 // compact [32][32] copy (row stride 32), wave-uniform, so every element is a
 // scalar load at a compile-time offset from one base pointer. Symmetric
@@ -188,19 +196,29 @@ __global__ void __launch_bounds__(kThreads)
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
   const bool sym = symflag[b * G + g] != 0;
 
-  float orig[kG];
-  load_group<TIn, IS_F16>(W, base, orig);
-  {  // dead columns (gptq.py:219-221) read as 0
+  // The group's 32 (dead-column-fixed) weights live in LDS, one column per
+  // thread (so[i][tid]: conflict-free), not in registers, which leaves room
+  // for 3 waves per SIMD without spills.
+  __shared__ float so[kG * kThreads];
+  float amax;
+  {
+    float v[kG];
+    load_group<TIn, IS_F16>(W, base, v);
+    // dead columns (gptq.py:219-221) read as 0
     const uint4 m0 = reinterpret_cast<const uint4*>(dd)[0];
     const uint4 m1 = reinterpret_cast<const uint4*>(dd)[1];
     const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
     for (int i = 0; i < kG; ++i)
-      if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) orig[i] = 0.0f;
-  }
-  float amax = fabsf(orig[0]);
+      if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) v[i] = 0.0f;
+    amax = fabsf(v[0]);
 #pragma unroll
-  for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(orig[i]));
+    for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(v[i]));
+#pragma unroll
+    for (int i = 0; i < kG; ++i) so[i * kThreads + threadIdx.x] = v[i];
+  }
+  const float* orig = so + threadIdx.x;  // orig[i * kThreads] = weight i
+#define ORIG(i) orig[(i) * kThreads]
 
   // 1. scale choice
   const int e0 = e8m0_exponent(amax, fmax);
@@ -213,7 +231,7 @@ __global__ void __launch_bounds__(kThreads)
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
       const float sc = exp2_int(e), inv = exp2_int(-e);
 #pragma unroll
-      for (int i = 0; i < kG; ++i) err[i] = quant_fast<MODE>(orig[i], inv, sc) - orig[i];
+      for (int i = 0; i < kG; ++i) err[i] = quant_fast<MODE>(ORIG(i), inv, sc) - ORIG(i);
       const float obj = quad_form(err, Hg + zero_after_s(err[0]), sym);
       if (o == 0 || obj < best) {
         best = obj;
@@ -229,20 +247,21 @@ __global__ void __launch_bounds__(kThreads)
   // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
   // Forming w_c lazily from the stored errors performs exactly those
   // roundings while keeping only err[] live.
-  float w[kG], errs[kG];
+  // The dequantized values are not kept: they are value(code) * scale,
+  // decoded again below, which keeps 32 registers free.
+  float errs[kG];
   uint32_t codes[kG / 4];
 #pragma unroll
   for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
   for (int c = 0; c < kG; ++c) {
     const float* col = Ut + c * kG + (c ? zero_after(errs[c - 1]) : 0);
-    float acc = orig[c];
+    float acc = ORIG(c);
 #pragma unroll
     for (int k = 0; k < c; ++k) acc = acc - errs[k] * col[k];
     float dq;
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
     errs[c] = (acc - dq) / col[c];
-    w[c] = dq;
     codes[c / 4] |= code << (8 * (c % 4));
   }
 
@@ -251,7 +270,7 @@ __global__ void __launch_bounds__(kThreads)
   if (SAFE) {
     float err[kG];
 #pragma unroll
-    for (int i = 0; i < kG; ++i) err[i] = w[i] - orig[i];
+    for (int i = 0; i < kG; ++i) err[i] = code_value<MODE>(codes, i, scale) - ORIG(i);
     use_gptq = quad_form(err, Hg + zero_after_s(err[kG - 1]), sym) <= best;
   }
   // 4. range guard on the selected result
@@ -261,17 +280,21 @@ __global__ void __launch_bounds__(kThreads)
   bool ok = use_gptq;
   if (use_gptq) {
 #pragma unroll
-    for (int i = 0; i < kG; ++i) ok = ok && (fabsf(w[i]) <= limit);
+    for (int i = 0; i < kG; ++i) ok = ok && (fabsf(code_value<MODE>(codes, i, scale)) <= limit);
   }
   if (!ok) {  // RTN baseline at the chosen scale
 #pragma unroll
     for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      const uint32_t code = quant_exact<MODE>(orig[i], inv_scale, scale, &w[i]);
+      float dq;
+      const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
       codes[i / 4] |= code << (8 * (i % 4));
     }
   }
+  float w[kG];
+#pragma unroll
+  for (int i = 0; i < kG; ++i) w[i] = code_value<MODE>(codes, i, scale);
 
   double num = 0.0, den = 0.0;
   if (valid) {
@@ -318,6 +341,8 @@ __global__ void __launch_bounds__(kThreads)
     }
   }
 }
+
+#undef ORIG
 
 // rel[b] = sqrt(sum num) / max(sqrt(sum den), 1e-12), partials summed in order.
 __global__ void rel_err_kernel(const double* __restrict__ part, int64_t n_per_b, int64_t B,
