@@ -1,22 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark: one MoE layer of GPTQ calibration on one MI355X.
+"""Benchmark: one layer of GPTQ calibration on one MI355X.
 
-Workload (the north-star target): a
+Default workload (the north-star target): a
 Qwen3-30B-A3B-shaped MoE layer -- 128 experts, hidden 2048,
 moe_intermediate 768, 131072 tokens routed top-8 -- solved end to end:
   per-expert Hessians (gate_up: routed gather of the hidden states, 2048^2;
   down: the experts' SiLU(g)*u inputs, 768^2), damped per-group Cholesky
   inverses, MXFP4 safe-scale-search GPTQ for every routed expert, RTN for
   the 4 unrouted experts (they have no Hessian), and MLX uint32 packing of
-  all codes. Inputs (hidden states, routing, expert weights) are synthetic,
-  seeded, and resident in HBM before the timed region.
+  all codes.
 
-One step = one layer. The JSON line reports weight elements solved per
-second, the Hessian kernel against the bf16 MFMA roofline, and the CPU
-oracle (the reference algorithm restated on torch-CPU) timed on a bounded
-sample of experts of the same workload.
+--config 1|2|3|5 runs the dense BASELINE configs instead (one Hessian per
+distinct input, GPTQ of every matrix in the config's mode, packing):
+  1 single Linear [2048,2048] affine 4-bit, 8192 tokens
+  2 q_proj [4096,4096] MXFP4 groupwise, 32768 tokens
+  3 up [14336,4096] + down [4096,14336] MXFP8 groupwise, 65536 tokens
+  5 gate, up [25600,5120] + down [5120,25600] MXFP4 safe search, 524288 tokens
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+Inputs (hidden states, routing, weights) are synthetic, seeded, and
+resident in HBM before the timed region. One step = one layer. The JSON
+line reports weight elements solved per second, the dominant kernel against
+its roofline, and the CPU oracle (the reference algorithm restated on
+torch-CPU) timed on a bounded sample of the same workload.
+
+Usage: python bench.py [--config 4] [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
 """
 
 from __future__ import annotations
@@ -32,10 +39,12 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-gptq-mxfp_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0
+MXFP_BYTES_PER_ELEMENT = 2 + 4 + 1 + 1 / 32  # bf16 W in, f32 W_dq + u8 code out, E8M0 scale
 
 
 def _args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--config", type=int, default=4, choices=(1, 2, 3, 4, 5))
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
@@ -48,37 +57,90 @@ def _args(argv=None):
     return ap.parse_args(argv)
 
 
-def _hessian_traffic():
-    """HBM bytes per gate_up Hessian launch (routed-gather SYRK kernel):
-    rocprofv3 FETCH_SIZE + WRITE_SIZE of that dispatch, each scaled by what
-    the counter reads for a plain 1 GiB copy, as committed under profiles/
-    (the profiler cannot run inside this process). None if absent."""
-    p = os.path.join(ROOT, "profiles", "bench_moe_cfg4_traffic.json")
+def _traffic(name: str, kernel_prefix: str):
+    """HBM bytes per launch of a kernel: rocprofv3 FETCH_SIZE + WRITE_SIZE of
+    that dispatch, each scaled by what the counter reads for a plain 1 GiB
+    copy, as committed under profiles/ (the profiler cannot run inside this
+    process). None if absent."""
+    p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         per = json.load(f).get("bytes_per_dispatch", {})
-    for k, v in per.items():
-        if k.startswith("mgq::syrk_dma_kernel<true>"):
-            return round(float(v))
-    return None
+    hits = [v for k, v in per.items() if k.startswith(kernel_prefix)]
+    return round(float(max(hits))) if hits else None
 
 
-def main(argv=None) -> int:
-    args = _args(argv)
-    if args.gpus != 1:
-        print(f"bench.py measures a single GPU (got --gpus {args.gpus}); multi-GPU runs are out of "
-              "scope for this build (experts shard across GPUs with no exchange)", file=sys.stderr)
-        return 2
+def _roofline(kernel, bound, amount, ms, traffic=None):
+    """amount: flops (bound "mfma") or bytes (bound "hbm") per launch."""
+    if bound == "mfma":
+        achieved, peak, unit = amount / (ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = amount / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+    return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+            "per_launch": amount, "launch_ms": round(ms, 4)}
 
-    import numpy as np
-    import torch
 
-    from mlx_gptq import _native, capture, gptq, grid, packing, synth
+def _copy_calibration(torch, dev, mib):
+    if mib <= 0:
+        return
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)  # reads and writes exactly n*4 bytes
+    torch.cuda.synchronize()
+    del src, dst
 
-    _native.load()
+
+def _timed(torch, np, step, n_phase, warmup, steps):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    phase = np.zeros(n_phase)
+    t0 = time.perf_counter()
+    out = None
+    for _ in range(steps):
+        out, evs = step()
+        torch.cuda.synchronize()  # events of this step are complete
+        phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(n_phase)]
+    t1 = time.perf_counter()
+    return out, (t1 - t0) * 1e3 / steps, phase / steps
+
+
+def _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, extra=None):
+    line = {
+        "metric": "GPTQ weight-elements solved/s per layer",
+        "value": round(value, 1),
+        "unit": "elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16+fp32",
+        "data": "synthetic (seeded hidden states, routing and weights of the config's shapes)",
+        "config": config,
+        "phases_ms": {k: round(float(v), 3) for k, v in phases.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "setup_s": round(setup_s, 2),
+    }
+    if extra:
+        line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# config 4: routed-expert MoE layer
+# ---------------------------------------------------------------------------
+def run_moe(args, torch, np) -> int:
+    from mlx_gptq import capture, gptq, grid, packing, synth
+
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
     t_setup = time.perf_counter()
     L = synth.moe_layer(device=dev)
     torch.cuda.synchronize()
@@ -108,82 +170,29 @@ def main(argv=None) -> int:
         rq_dn, rs_dn, _, _ = grid.rtn_quantize_mxfp(L.W_down[ne:], "mxfp4")
         packed = [packing.pack_q(q, 4) for q in (q_gu, q_dn, rq_gu, rq_dn)]
         evs[5].record()
-        return q_gu, s_gu, q_dn, s_dn, packed
+        return (q_gu, s_gu, q_dn, s_dn, packed), evs
 
-    if args.copy_calib_mib > 0:
-        n = args.copy_calib_mib * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.neg(src, out=dst)  # reads and writes exactly n*4 bytes
-        torch.cuda.synchronize()
-        del src, dst
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    phase = np.zeros(5)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = step()
-        torch.cuda.synchronize()  # events of this step are complete
-        phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(5)]
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    phase /= args.steps
+    _copy_calibration(torch, dev, args.copy_calib_mib)
+    out, ms_step, phase = _timed(torch, np, step, 5, args.warmup, args.steps)
     value = elements / (ms_step * 1e-3)
-
-    hess_flops = A * hidden * (hidden + 1)  # SYRK count N*C*(C+1), gate_up launch
-    hess_ms = float(phase[0])
-    achieved = hess_flops / (hess_ms * 1e-3) / 1e12
-    roofline = {
-        "kernel": "syrk_dma_kernel (gate_up Hessian, routed gather)",
-        "bound": "mfma",
-        "achieved": round(achieved, 1),
-        "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": _hessian_traffic(),
-        "flops_per_launch": hess_flops,
-        "launch_ms": round(hess_ms, 4),
+    roofline = _roofline("syrk_dma_kernel (gate_up Hessian, routed gather)", "mfma",
+                         A * hidden * (hidden + 1),  # SYRK count N*C*(C+1)
+                         float(phase[0]), _traffic("bench_moe_cfg4", "mgq::syrk_dma_kernel<true>"))
+    cpu = _cpu_baseline_moe(L, ne, out, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    config = {
+        "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
+                    "[2048,768]), 131072 tokens top-8, MXFP4 safe-scale-search GPTQ, 4 unrouted "
+                    "experts RTN, uint32 pack",
+        "experts": E, "hidden": hidden, "moe_intermediate": inter, "tokens": L.X.shape[0],
+        "top_k": A // L.X.shape[0], "assignments": A, "elements": elements,
     }
-
-    cpu = None
-    if args.cpu_seconds > 0:
-        cpu = _cpu_baseline(L, ne, out, args.cpu_seconds)
-
-    line = {
-        "metric": "GPTQ weight-elements solved/s per layer",
-        "value": round(value, 1),
-        "unit": "elements/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16+fp32",
-        "data": "synthetic (seeded hidden states, router, expert weights)",
-        "config": {
-            "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
-                        "[2048,768]), 131072 tokens top-8, MXFP4 safe-scale-search GPTQ, 4 unrouted "
-                        "experts RTN, uint32 pack",
-            "experts": E, "hidden": hidden, "moe_intermediate": inter, "tokens": L.X.shape[0],
-            "top_k": A // L.X.shape[0], "assignments": A, "elements": elements,
-        },
-        "phases_ms": {"hessian_gate_up": round(float(phase[0]), 3), "hessian_down": round(float(phase[1]), 3),
-                      "solve_gate_up": round(float(phase[2]), 3), "solve_down": round(float(phase[3]), 3),
-                      "rtn_and_pack": round(float(phase[4]), 3)},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "setup_s": round(setup_s, 2),
-    }
-    print(json.dumps(line), flush=True)
+    phases = {"hessian_gate_up": phase[0], "hessian_down": phase[1], "solve_gate_up": phase[2],
+              "solve_down": phase[3], "rtn_and_pack": phase[4]}
+    _line(args, value, ms_step, config, phases, roofline, cpu, setup_s)
     return 0
 
 
-def _cpu_baseline(L, ne, gpu_out, budget_s):
+def _cpu_baseline_moe(L, ne, gpu_out, budget_s):
     """Time the CPU oracle on whole experts of the same layer until the budget
     is spent; also report code agreement with the GPU on those experts."""
     import torch
@@ -191,7 +200,6 @@ def _cpu_baseline(L, ne, gpu_out, budget_s):
     sys.path.insert(0, ROOT)
     from oracle import gptq_ref, hessian_ref, packing_ref
 
-    torch.set_num_threads(max(1, torch.get_num_threads()))
     hidden, inter = L.W_gate_up.shape[2], L.W_down.shape[2]
     q_gu, _, q_dn, _, _ = gpu_out
     spent, done, elems, agree_n, agree_d = 0.0, 0, 0, 0, 0
@@ -226,6 +234,145 @@ def _cpu_baseline(L, ne, gpu_out, budget_s):
                   f"Hessian (fp32 addmm) + Cholesky + MXFP4 safe-search GPTQ + pack, {spent:.1f} s",
         "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
     }
+
+
+# ---------------------------------------------------------------------------
+# configs 1, 2, 3, 5: dense layers
+# ---------------------------------------------------------------------------
+def run_dense(args, torch, np) -> int:
+    from mlx_gptq import capture, gptq, packing, synth
+
+    dev = torch.device("cuda", 0)
+    t_setup = time.perf_counter()
+    L = synth.dense_config(args.config, device=dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    keys = list(L.inputs)
+    Hs = {k: torch.empty(1, X.shape[1], X.shape[1], dtype=torch.float32, device=dev)
+          for k, X in L.inputs.items()}
+    n_ev = len(keys) + len(L.mats) + 1
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
+
+    def step():
+        i = 0
+        evs[i].record()
+        for k in keys:
+            capture.hessian_xtx(L.inputs[k], out=Hs[k][0])
+            i += 1
+            evs[i].record()
+        res = []
+        for m in L.mats:
+            res.append(gptq.solve_gptq(m.W, Hs[m.inp], **m.solve))
+            i += 1
+            evs[i].record()
+        packed = [packing.pack_q(r[0], m.pack_bits) for r, m in zip(res, L.mats)]
+        i += 1
+        evs[i].record()
+        return (res, packed), evs
+
+    _copy_calibration(torch, dev, args.copy_calib_mib)
+    out, ms_step, phase = _timed(torch, np, step, n_ev, args.warmup, args.steps)
+    elements = L.elements
+    value = elements / (ms_step * 1e-3)
+    phases, rooflines = {}, {}
+    tag = f"bench_dense_cfg{args.config}"
+    for i, k in enumerate(keys):
+        N, C = L.inputs[k].shape
+        phases[f"hessian_{k}"] = phase[i]
+        rooflines[f"hessian_{k}"] = _roofline(f"syrk_dma_kernel (Hessian of '{k}', [{N}x{C}])", "mfma",
+                                              N * C * (C + 1), float(phase[i]),
+                                              _traffic(f"{tag}_{k}", "mgq::syrk_dma_kernel<false>"))
+    for j, m in enumerate(L.mats):
+        ms = float(phase[len(keys) + j])
+        phases[f"solve_{m.name}"] = ms
+        n = int(m.W.numel())
+        if m.solve["mode"] == "affine":
+            byt = n * (2 + 4 + 1 + 4 / m.solve["group_size"])
+        else:
+            byt = n * MXFP_BYTES_PER_ELEMENT
+        rooflines[f"solve_{m.name}"] = _roofline(f"GPTQ solve '{m.name}' ({m.solve['mode']})", "hbm",
+                                                 byt, ms)
+    phases["pack"] = phase[-1]
+    dom = max(rooflines, key=lambda k: rooflines[k]["launch_ms"])
+    cpu = _cpu_baseline_dense(L, out, Hs, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    config = {"workload": L.name, "elements": elements,
+              "matrices": {m.name: list(m.W.shape[1:]) for m in L.mats},
+              "tokens": {k: int(X.shape[0]) for k, X in L.inputs.items()}}
+    _line(args, value, ms_step, config, phases, rooflines[dom], cpu, setup_s,
+          {"phase_rooflines": rooflines})
+    return 0
+
+
+def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
+    """CPU oracle on a bounded sample, extrapolated linearly: the Hessian on
+    the first tokens of each input (its cost is linear in tokens) and the
+    solve + pack on the first rows of each matrix with the full Hessian (the
+    column loops are elementwise over rows; the O(C^3) Cholesky of the affine
+    path is timed once and not scaled)."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import gptq_ref, hessian_ref, packing_ref
+
+    res, _ = gpu_out
+    t_total, agree_n, agree_d, parts = 0.0, 0, 0, []
+    per_budget = budget_s / (len(L.inputs) + len(L.mats))
+    for k, X in L.inputs.items():
+        N, C = X.shape
+        n_s = int(min(N, max(256, per_budget * 0.9e12 / (2.0 * C * C))))
+        xs = X[:n_s].cpu()
+        t = time.perf_counter()
+        hessian_ref.stash_hessian([xs], C)
+        dt = time.perf_counter() - t
+        t_total += dt * N / n_s
+        parts.append(f"Hessian '{k}' on {n_s}/{N} tokens")
+    for m, r in zip(L.mats, res):
+        R, C = m.W.shape[1:]
+        kw = dict(m.solve)
+        H = Hs[m.inp].cpu()
+        hinv_t = 0.0
+        if kw["mode"] == "affine":  # the full-matrix factor is per layer, not per row
+            t = time.perf_counter()
+            gptq_ref.prepare_hinv(H.clone(), 0.01)
+            hinv_t = time.perf_counter() - t
+        r_s = R if kw["mode"] == "affine" else int(min(R, 2048))
+        Ws = m.W[0, :r_s].unsqueeze(0).cpu()
+        t = time.perf_counter()
+        rq = gptq_ref.solve_gptq(Ws, H.clone(), **kw)[0]
+        packing_ref.pack_q(rq[0].numpy(), m.pack_bits)
+        dt = time.perf_counter() - t
+        t_total += hinv_t + max(dt - hinv_t, 0.0) * R / r_s
+        agree_n += int((r[0][0, :r_s].cpu() == rq[0]).sum())
+        agree_d += rq.numel()
+        parts.append(f"solve+pack '{m.name}' on {r_s}/{R} rows")
+    return {
+        "value": round(L.elements / t_total, 1),
+        "unit": "elements/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": "CPU oracle, extrapolated linearly from " + "; ".join(parts)
+                  + f" (estimated {t_total:.1f} s per layer)",
+        "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
+    }
+
+
+def main(argv=None) -> int:
+    args = _args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures a single GPU (got --gpus {args.gpus}); multi-GPU runs are out of "
+              "scope for this build (experts shard across GPUs with no exchange)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from mlx_gptq import _native
+
+    _native.load()
+    torch.cuda.set_device(torch.device("cuda", 0))
+    if args.config == 4:
+        return run_moe(args, torch, np)
+    return run_dense(args, torch, np)
 
 
 if __name__ == "__main__":

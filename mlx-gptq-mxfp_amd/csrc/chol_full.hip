@@ -4,20 +4,25 @@
 //   U (upper) with U^T U = (H + lam I)^-1,  lam = damp * max(mean(diag H), 1e-8)
 //
 // As in the 32x32 kernel, Hd = V V^T is factored with V upper triangular
-// ("UL" Cholesky, i.e. Cholesky in reverse index order) and U = V^-1. The
-// blocked algorithm walks diagonal blocks of nb = 64 from the bottom-right
-// corner to the top-left; for the block at jb (A11 = A[0:jb,0:jb],
-// A12 = A[0:jb, jb:jb+nb], A22 = the diagonal block):
-//   1. A22 = V22 V22^T (one workgroup, fp64 in LDS), W22 = V22^-1;
-//   2. V12 = A12 W22^T                                 (panel);
-//   3. A11 -= V12 V12^T  (upper triangle)              (trailing update);
-//   4. W[jb:jb+nb, jb+nb:] = -W22 V[jb:jb+nb, jb+nb:] W[jb+nb:, jb+nb:]
-//      (the inverse grows upward with the factor: W = V^-1 is upper).
-// Everything runs in fp64 (the factor of an fp32 matrix, rounded once), on
-// a per-batch-item fp64 workspace. Items whose pivot fails are flagged and
-// skipped by later steps; the host escalates their damping and reruns them,
-// exactly like the reference retries only the failed batch items.
+// ("UL" Cholesky, i.e. Cholesky in reverse index order) and U = V^-1 = W.
+// The factor and its inverse are built together by recursion over 64-row
+// blocks [b0, b1), split at mid (top rows T = [b0, mid), bottom rows
+// S = [mid, b1)):
+//   1. (V_SS, W_SS) of A_SS                          (recursion, bottom first)
+//   2. P = V_TS = A_TS W_SS^T                        (GEMM)
+//   3. A_TT -= P P^T                                 (GEMM, upper tiles)
+//   4. Q = P W_SS                                    (GEMM)
+//   5. (V_TT, W_TT) of the updated A_TT              (recursion)
+//   6. W_TS = -W_TT Q                                (GEMM)
+// since V V^T = [[V_TT V_TT^T + V_TS V_TS^T, V_TS V_SS^T], [., V_SS V_SS^T]]
+// and V^-1 = [[W_TT, -W_TT V_TS W_SS], [0, W_SS]]. A 64x64 leaf is factored
+// and inverted by one workgroup with the block in registers. Everything runs
+// in fp64 (the factor of an fp32 matrix, rounded to fp32 once). Items whose
+// pivot fails are flagged and skipped by later steps; the host escalates
+// their damping and reruns them, exactly like the reference retries only the
+// failed batch items.
 #include <algorithm>
+#include <vector>
 
 #include "mgq_capi.h"
 #include "mgq_common.h"
@@ -25,247 +30,255 @@
 namespace mgq {
 namespace {
 
-constexpr int kNb = 64;
+constexpr int kNb = 64;  // leaf block
+constexpr int kGT = 64;  // GEMM output tile edge
 
-// A = fp64(H + lam I) for items with active[b]; lam from fp32 ops as the
-// reference forms Hd (diag_mean * damp, then diag += lam).
-__global__ void build_hd_kernel(const float* __restrict__ H, int64_t C,
-                                const float* __restrict__ damp, const uint8_t* __restrict__ active,
-                                double* __restrict__ A) {
+// lam[b] = fp32(max(mean(diag H_b), 1e-8) * damp[b]): fp64 diagonal sum
+// rounded once, then the reference's fp32 clamp and product.
+__global__ void __launch_bounds__(256)
+    lam_kernel(const float* __restrict__ H, int64_t C, const float* __restrict__ damp,
+               const uint8_t* __restrict__ active, float* __restrict__ lam) {
+  const int64_t b = blockIdx.x;
+  if (!active[b]) return;
+  __shared__ double part[256];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < C; i += 256) s += static_cast<double>(H[b * C * C + i * C + i]);
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float dm = static_cast<float>(part[0] / static_cast<double>(C));
+    dm = dm < 1e-8f ? 1e-8f : dm;  // NaN stays NaN
+    lam[b] = dm * damp[b];
+  }
+}
+
+// A = fp64(H + lam I) (diagonal added in fp32, as the reference forms Hd);
+// W = 0 (its blocks below the block diagonal must read as zero).
+__global__ void build_kernel(const float* __restrict__ H, int64_t C, const float* __restrict__ lam,
+                             const uint8_t* __restrict__ active, double* __restrict__ A,
+                             double* __restrict__ W) {
   const int64_t b = blockIdx.y;
   if (!active[b]) return;
+  const float l = lam[b];
   const float* Hb = H + b * C * C;
   double* Ab = A + b * C * C;
-  // diag mean: fp64 sum, rounded once, clamped at 1e-8 (NaN stays NaN)
-  __shared__ float s_lam;
-  if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int64_t i = 0; i < C; ++i) s += static_cast<double>(Hb[i * C + i]);
-    float dm = static_cast<float>(s / static_cast<double>(C));
-    dm = dm < 1e-8f ? 1e-8f : dm;
-    s_lam = dm * damp[b];
-  }
-  __syncthreads();
-  const float lam = s_lam;
+  double* Wb = W + b * C * C;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < C * C;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / C, j = e % C;
     float v = Hb[e];
-    if (i == j) v = v + lam;
+    if (e / C == e % C) v = v + l;
     Ab[e] = static_cast<double>(v);
+    Wb[e] = 0.0;
   }
 }
 
-// Step 1: factor the diagonal block at jb (size n <= 64) in LDS; write V22
-// into A's block and W22 = V22^-1 into W's block. A failed pivot sets
-// failed[b].
+// Leaf: the n x n (n <= 64) diagonal block at r0, 256 threads, the block
+// in registers as 4x4 tiles (thread (tr, tc) owns rows 4tr.., columns
+// 4tc..). Right-looking UL factor from the last column:
+//   V[j][j] = sqrt(M[j][j]),  V[i][j] = M[i][j] / V[j][j]  (i < j),
+//   M[i][k] -= V[i][j] V[k][j]  (i <= k < j),
+// with column j broadcast through LDS; then W = V^-1 by back substitution
+// on X = I:  W[r][:] = X[r][:] / V[r][r],  X[i][:] -= V[i][r] W[r][:] (i < r).
+// Broadcast buffers alternate between steps, so each step needs two
+// barriers. Entries below the diagonal of M are never read. Writes W's
+// block (zeros below the diagonal).
 __global__ void __launch_bounds__(256)
-    diag_block_kernel(double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t jb, int n,
-                      const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
+    leaf_kernel(const double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t r0, int n,
+                const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
   const int64_t b = blockIdx.x;
   if (!active[b] || failed[b]) return;
-  __shared__ double S[kNb][kNb + 1];
-  __shared__ double Wi[kNb][kNb + 1];
-  __shared__ int s_fail;
-  double* Ab = A + b * C * C;
-  double* Wb = W + b * C * C;
   const int tid = threadIdx.x;
-  for (int e = tid; e < n * n; e += blockDim.x) {
-    const int i = e / n, j = e % n;
-    S[i][j] = Ab[(jb + i) * C + jb + j];
-  }
-  if (tid == 0) s_fail = 0;
-  __syncthreads();
-  for (int j = n - 1; j >= 0; --j) {
-    const double d = S[j][j];
-    if (!(d > 0.0)) {
-      if (tid == 0) s_fail = 1;
-      break;  // uniform: every thread read the same pivot after the barrier
+  const int tr = tid >> 4, tc = tid & 15;
+  __shared__ double piv[2];
+  __shared__ double colv[2][kNb];
+  __shared__ double wrow[2][kNb];
+  const double* Ab = A + b * C * C + r0 * C + r0;
+  double a[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tr * 4 + p, k = tc * 4 + q;
+      a[p][q] = (i < n && k < n) ? Ab[i * C + k] : 0.0;
     }
-    const double s = sqrt(d);
-    __syncthreads();
-    if (tid < j) S[tid][j] = S[tid][j] / s;
-    if (tid == 0) S[j][j] = s;
-    __syncthreads();
-    for (int e = tid; e < j * j; e += blockDim.x) {
-      const int i = e / j, k = e % j;
-      if (i <= k) S[i][k] = S[i][k] - S[i][j] * S[k][j];
+  // columns in groups of 4 so the column inside a tile is a constant (the
+  // register arrays stay in registers)
+  for (int jb = (n - 1) >> 2; jb >= 0; --jb) {
+#pragma unroll
+    for (int jq = 3; jq >= 0; --jq) {
+      const int j = jb * 4 + jq;
+      if (j >= n) continue;  // uniform
+      const int par = j & 1;
+      if (tr == jb && tc == jb) piv[par] = a[jq][jq];
+      __syncthreads();
+      const double d = piv[par];
+      if (!(d > 0.0)) {  // uniform
+        if (tid == 0) failed[b] = 1;
+        return;
+      }
+      const double sd = sqrt(d);
+      const double rs = 1.0 / sd;  // fp64: scaling by the reciprocal is exact to ~1 ulp
+      if (tc == jb) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int i = tr * 4 + p;
+          const double v = i < j ? a[p][jq] * rs : (i == j ? sd : 0.0);
+          colv[par][i] = v;
+          if (i <= j) a[p][jq] = v;
+        }
+      }
+      __syncthreads();
+      double ci[4], ck[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) ci[p] = colv[par][tr * 4 + p];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ck[q] = colv[par][tc * 4 + q];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = tr * 4 + p, k = tc * 4 + q;
+          if (i <= k && k < j) a[p][q] = a[p][q] - ci[p] * ck[q];
+        }
     }
-    __syncthreads();
   }
-  __syncthreads();
-  if (s_fail) {
-    if (tid == 0) failed[b] = 1;
-    return;
-  }
-  // W22 = V22^-1 (upper), thread j back-substitutes column j
-  if (tid < n) {
-    const int j = tid;
-    Wi[j][j] = 1.0 / S[j][j];
-    for (int i = j - 1; i >= 0; --i) {
-      double acc = 0.0;
-      for (int k = i + 1; k <= j; ++k) acc += S[i][k] * Wi[k][j];
-      Wi[i][j] = -acc / S[i][i];
+  // X = I, then back substitution; V's column r comes from a (final).
+  double x[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[p][q] = (tr * 4 + p == tc * 4 + q) ? 1.0 : 0.0;
+  for (int rb = (n - 1) >> 2; rb >= 0; --rb) {
+#pragma unroll
+    for (int rq = 3; rq >= 0; --rq) {
+      const int r = rb * 4 + rq;
+      if (r >= n) continue;  // uniform
+      const int par = r & 1;
+      if (tc == rb) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) colv[par][tr * 4 + p] = a[p][rq];  // V[i][r]
+      }
+      __syncthreads();
+      if (tr == rb) {
+        const double ivr = 1.0 / colv[par][r];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wrow[par][tc * 4 + q] = x[rq][q] * ivr;
+      }
+      __syncthreads();
+      double vi[4], wc[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) vi[p] = colv[par][tr * 4 + p];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wc[q] = wrow[par][tc * 4 + q];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int i = tr * 4 + p;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (i < r) x[p][q] = x[p][q] - vi[p] * wc[q];
+          else if (i == r) x[p][q] = wc[q];
+        }
+      }
     }
   }
-  __syncthreads();
-  for (int e = tid; e < n * n; e += blockDim.x) {
-    const int i = e / n, j = e % n;
-    Ab[(jb + i) * C + jb + j] = (i <= j) ? S[i][j] : 0.0;
-    Wb[(jb + i) * C + jb + j] = (i <= j) ? Wi[i][j] : 0.0;
+  double* Wb = W + b * C * C + r0 * C + r0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tr * 4 + p, k = tc * 4 + q;
+      if (i < n && k < n) Wb[i * C + k] = x[p][q];
+    }
+}
+
+// C[m][n] = alpha * sum_k A[m][k] opB[k][n] + beta * C[m][n], opB = B or B^T
+// (B stored [N][K]); row-major with leading dimensions, one matrix per batch
+// item (item strides sA, sB, sC). 64x64 output tiles, 4x4 per thread; K in
+// chunks of 32 staged through LDS, the next chunk's global loads in flight
+// (registers) while the current one is multiplied. UPPER skips tiles
+// strictly below the diagonal.
+constexpr int kGK2 = 32;
+
+template <bool TRANSB>
+__device__ inline void gemm_load(const double* __restrict__ Ab, int64_t lda,
+                                 const double* __restrict__ Bb, int64_t ldb, int M, int N, int K,
+                                 int m0, int n0, int k0, int tid, double (&ra)[8],
+                                 double (&rb)[8]) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = tid + q * 256;  // 64 x 32 elements
+    const int m = e / kGK2, kk = e % kGK2;
+    ra[q] = (m0 + m < M && k0 + kk < K) ? Ab[(int64_t)(m0 + m) * lda + k0 + kk] : 0.0;
+    if (TRANSB) {
+      rb[q] = (n0 + m < N && k0 + kk < K) ? Bb[(int64_t)(n0 + m) * ldb + k0 + kk] : 0.0;
+    } else {
+      const int kr = e / kGT, nn = e % kGT;
+      rb[q] = (n0 + nn < N && k0 + kr < K) ? Bb[(int64_t)(k0 + kr) * ldb + n0 + nn] : 0.0;
+    }
   }
 }
 
-// Step 2: V12 = A12 * W22^T, rows 0..jb-1, cols jb..jb+n-1 (in place in A).
-// One thread per (row, col); the row of A12 is staged in registers first.
-__global__ void panel_kernel(double* __restrict__ A, const double* __restrict__ W, int64_t C,
-                             int64_t jb, int n, const uint8_t* __restrict__ active,
-                             const uint8_t* __restrict__ failed) {
-  const int64_t b = blockIdx.y;
-  if (!active[b] || failed[b]) return;
-  double* Ab = A + b * C * C;
-  const double* Wb = W + b * C * C;
-  __shared__ double Wt[kNb][kNb + 1];  // W22
-  for (int e = threadIdx.x; e < n * n; e += blockDim.x) Wt[e / n][e % n] = Wb[(jb + e / n) * C + jb + e % n];
-  __syncthreads();
-  const int64_t rows_per_block = blockDim.x / kNb;
-  const int64_t i = blockIdx.x * rows_per_block + threadIdx.x / kNb;
-  const int c = threadIdx.x % kNb;
-  __shared__ double Arow[4][kNb];
-  const int slot = threadIdx.x / kNb;
-  if (i < jb && c < n) Arow[slot][c] = Ab[i * C + jb + c];
-  __syncthreads();
-  if (i < jb && c < n) {
-    // V12[i][c] = sum_k A12[i][k] * W22[c][k]  (W22 upper: k >= c)
-    double acc = 0.0;
-    for (int k = c; k < n; ++k) acc += Arow[slot][k] * Wt[c][k];
-    Ab[i * C + jb + c] = acc;
-  }
-}
-
-// Step 3: A11[i][k] -= sum_c V12[i][c] V12[k][c] for i <= k < jb. 64x64
-// output tiles (upper-triangular tiles only), 4x4 outputs per thread, the
-// two V12 row panels staged in LDS (K = n <= 64).
+template <bool TRANSB, bool UPPER>
 __global__ void __launch_bounds__(256)
-    trailing_kernel(double* __restrict__ A, int64_t C, int64_t jb, int n,
-                    const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
-  const int64_t b = blockIdx.z;
-  if (!active[b] || failed[b]) return;
-  const int64_t ti = blockIdx.y, tk = blockIdx.x;
-  if (tk < ti) return;  // upper tiles only
-  double* Ab = A + b * C * C;
-  __shared__ double Pi[kNb][kNb + 1], Pk[kNb][kNb + 1];  // [c][row]
+    dgemm_kernel(const double* __restrict__ A, int64_t lda, int64_t sA,
+                 const double* __restrict__ B, int64_t ldb, int64_t sB, double* __restrict__ Cm,
+                 int64_t ldc, int64_t sC, int M, int N, int K, double alpha, double beta,
+                 const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
+  const int64_t item = blockIdx.z;
+  if (!active[item] || failed[item]) return;
+  const int m0 = blockIdx.y * kGT, n0 = blockIdx.x * kGT;
+  if (UPPER && n0 + kGT <= m0) return;
+  const double* Ab = A + item * sA;
+  const double* Bb = B + item * sB;
+  double* Cb = Cm + item * sC;
+  __shared__ double As[kGK2][kGT + 1];
+  __shared__ double Bs[kGK2][kGT + 1];
   const int tid = threadIdx.x;
-  for (int e = tid; e < kNb * kNb; e += 256) {
-    const int r = e / kNb, c = e % kNb;
-    const int64_t ri = ti * kNb + r, rk = tk * kNb + r;
-    Pi[c][r] = (ri < jb && c < n) ? Ab[ri * C + jb + c] : 0.0;
-    Pk[c][r] = (rk < jb && c < n) ? Ab[rk * C + jb + c] : 0.0;
-  }
-  __syncthreads();
   const int tx = tid % 16, ty = tid / 16;
   double acc[4][4] = {};
-  for (int c = 0; c < n; ++c) {
-    double pi[4], pk[4];
+  double ra[8], rb[8];
+  gemm_load<TRANSB>(Ab, lda, Bb, ldb, M, N, K, m0, n0, 0, tid, ra, rb);
+  for (int k0 = 0; k0 < K; k0 += kGK2) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a) pi[a] = Pi[c][ty * 4 + a];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) pk[a] = Pk[c][tx * 4 + a];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) acc[a][d] += pi[a] * pk[d];
-  }
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t i = ti * kNb + ty * 4 + a;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int64_t k = tk * kNb + tx * 4 + d;
-      if (i < jb && k < jb && i <= k) Ab[i * C + k] -= acc[a][d];
-    }
-  }
-}
-
-// Step 4: W[jb+r][m] = -sum_q W22[r][q] * T[q][m] for m >= jb+n, with
-// T[q][m] = sum_{k=jb+n}^{m} V[jb+q][k] * W[k][m] (W upper: terms k > m are
-// zero and are masked, since W's lower blocks are never written). One block
-// per 64-column tile: T by a K-chunked LDS GEMM, then the 64x64 product
-// with W22, 4x4 outputs per thread in both.
-constexpr int kKc = 16;
-
-__global__ void __launch_bounds__(256)
-    wrow_kernel(const double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t jb, int n,
-                const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
-  const int64_t b = blockIdx.y;
-  if (!active[b] || failed[b]) return;
-  const double* Ab = A + b * C * C;
-  double* Wb = W + b * C * C;
-  const int64_t m0 = jb + n + static_cast<int64_t>(blockIdx.x) * kNb;  // column tile
-  if (m0 >= C) return;
-  __shared__ double Vs[kKc][kNb + 1];  // [kk][q]
-  __shared__ double Ws[kKc][kNb + 1];  // [kk][mm]
-  __shared__ double T[kNb][kNb + 1];   // [q][mm]
-  __shared__ double Wd[kNb][kNb + 1];  // W22 transposed: Wd[q][r] = W22[r][q]
-  const int tid = threadIdx.x;
-  const int tx = tid % 16, ty = tid / 16;
-  const int64_t kend = (m0 + kNb < C) ? m0 + kNb : C;
-  double acc[4][4] = {};
-  for (int64_t k0 = jb + n; k0 < kend; k0 += kKc) {
-    for (int e = tid; e < kKc * kNb; e += 256) {
-      const int q = e / kKc, kk = e % kKc;
-      const int64_t k = k0 + kk;
-      Vs[kk][q] = (q < n && k < kend) ? Ab[(jb + q) * C + k] : 0.0;
-    }
-    for (int e = tid; e < kKc * kNb; e += 256) {
-      const int kk = e / kNb, mm = e % kNb;
-      const int64_t k = k0 + kk, m = m0 + mm;
-      Ws[kk][mm] = (k < kend && m < C && k <= m) ? Wb[k * C + m] : 0.0;
+    for (int q = 0; q < 8; ++q) {
+      const int e = tid + q * 256;
+      As[e % kGK2][e / kGK2] = ra[q];
+      if (TRANSB) {
+        Bs[e % kGK2][e / kGK2] = rb[q];
+      } else {
+        Bs[e / kGT][e % kGT] = rb[q];
+      }
     }
     __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < kKc; ++kk) {
-      double v[4], w[4];
+    if (k0 + kGK2 < K) gemm_load<TRANSB>(Ab, lda, Bb, ldb, M, N, K, m0, n0, k0 + kGK2, tid, ra, rb);
+#pragma unroll 8
+    for (int kk = 0; kk < kGK2; ++kk) {
+      double av[4], bv[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) v[a] = Vs[kk][ty * 4 + a];
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) w[a] = Ws[kk][tx * 4 + a];
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) acc[a][d] += v[a] * w[d];
+        for (int j = 0; j < 4; ++j) acc[i][j] = fma(av[i], bv[j], acc[i][j]);
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= M) continue;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) T[ty * 4 + a][tx * 4 + d] = acc[a][d];
-  for (int e = tid; e < kNb * kNb; e += 256) {
-    const int r = e / kNb, q = e % kNb;
-    Wd[q][r] = (r < n && q < n) ? Wb[(jb + r) * C + jb + q] : 0.0;
-  }
-  __syncthreads();
-  double out[4][4] = {};
-  for (int q = 0; q < n; ++q) {
-    double wr[4], t[4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) wr[a] = Wd[q][ty * 4 + a];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) t[d] = T[q][tx * 4 + d];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) out[a][d] += wr[a] * t[d];
-  }
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int r = ty * 4 + a;
-    if (r >= n) continue;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int64_t m = m0 + tx * 4 + d;
-      if (m < C) Wb[(jb + r) * C + m] = -out[a][d];
+    for (int j = 0; j < 4; ++j) {
+      const int nn = n0 + tx * 4 + j;
+      if (nn >= N) continue;
+      double* p = Cb + (int64_t)m * ldc + nn;
+      *p = beta == 0.0 ? alpha * acc[i][j] : alpha * acc[i][j] + beta * *p;
     }
   }
 }
@@ -278,9 +291,98 @@ __global__ void emit_u_kernel(const double* __restrict__ W, int64_t C,
   if (!active[b] || failed[b]) return;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < C * C;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / C, j = e % C;
-    U[b * C * C + e] = (i <= j) ? static_cast<float>(W[b * C * C + e]) : 0.0f;
+    U[b * C * C + e] = (e / C <= e % C) ? static_cast<float>(W[b * C * C + e]) : 0.0f;
   }
+}
+
+// Workspace plan: A, W (B x C x C fp64 each), lam (B floats), P (largest
+// top x bottom block product) and one Q slot per recursion depth.
+struct Layout {
+  int64_t lam_off, p_off, q_off[32], total;
+  int64_t p_elems, q_elems[32];
+};
+
+void plan_sizes(int64_t b0, int64_t b1, int64_t C, int depth, Layout* L) {
+  if (b1 - b0 <= 1) return;
+  const int64_t mid = b0 + (b1 - b0) / 2;
+  const int64_t r0 = b0 * kNb, rm = mid * kNb, r1 = std::min(b1 * kNb, C);
+  const int64_t hs = (rm - r0) * (r1 - rm);
+  L->p_elems = std::max(L->p_elems, hs);
+  L->q_elems[depth] = std::max(L->q_elems[depth], hs);
+  plan_sizes(mid, b1, C, depth + 1, L);
+  plan_sizes(b0, mid, C, depth + 1, L);
+}
+
+Layout make_layout(int64_t B, int64_t C) {
+  Layout L{};
+  const int64_t nblk = ceil_div(C, kNb);
+  plan_sizes(0, nblk, C, 0, &L);
+  int64_t off = 2 * B * C * C * 8;
+  L.lam_off = off;
+  off += ceil_div(B * 4, 256) * 256;
+  L.p_off = off;
+  off += B * L.p_elems * 8;
+  for (int d = 0; d < 32; ++d) {
+    L.q_off[d] = off;
+    off += B * L.q_elems[d] * 8;
+  }
+  L.total = off + 256;
+  return L;
+}
+
+struct Ctx {
+  double* A;
+  double* W;
+  double* P;
+  double* Q[32];
+  int64_t B, C;
+  const uint8_t* active;
+  uint8_t* failed;
+  hipStream_t s;
+};
+
+template <bool TRANSB, bool UPPER = false>
+int gemm(const Ctx& x, const double* A, int64_t lda, int64_t sA, const double* Bm, int64_t ldb,
+         int64_t sB, double* Cm, int64_t ldc, int64_t sC, int64_t M, int64_t N, int64_t K,
+         double alpha, double beta) {
+  dim3 grid(static_cast<unsigned>(ceil_div(N, kGT)), static_cast<unsigned>(ceil_div(M, kGT)),
+            static_cast<unsigned>(x.B));
+  dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(A, lda, sA, Bm, ldb, sB, Cm, ldc, sC,
+                                                     static_cast<int>(M), static_cast<int>(N),
+                                                     static_cast<int>(K), alpha, beta, x.active,
+                                                     x.failed);
+  return check_launch("hinv gemm");
+}
+
+int factor_rec(const Ctx& x, int64_t b0, int64_t b1, int depth) {
+  const int64_t C = x.C, CC = C * C;
+  const int64_t r0 = b0 * kNb, r1 = std::min(b1 * kNb, C);
+  if (b1 - b0 == 1) {
+    leaf_kernel<<<static_cast<unsigned>(x.B), 256, 0, x.s>>>(x.A, x.W, C, r0,
+                                                            static_cast<int>(r1 - r0), x.active,
+                                                            x.failed);
+    return check_launch("hinv leaf");
+  }
+  const int64_t mid = b0 + (b1 - b0) / 2;
+  const int64_t rm = mid * kNb, h = rm - r0, s2 = r1 - rm;
+  if (int rc = factor_rec(x, mid, b1, depth + 1)) return rc;
+  const double* Wss = x.W + rm * C + rm;
+  // P = A_TS W_SS^T
+  if (int rc = gemm<true>(x, x.A + r0 * C + rm, C, CC, Wss, C, CC, x.P, s2, h * s2, h, s2, s2,
+                          1.0, 0.0))
+    return rc;
+  // A_TT -= P P^T (upper tiles)
+  if (int rc = gemm<true, true>(x, x.P, s2, h * s2, x.P, s2, h * s2, x.A + r0 * C + r0, C, CC, h,
+                                h, s2, -1.0, 1.0))
+    return rc;
+  // Q = P W_SS
+  double* Q = x.Q[depth];
+  if (int rc = gemm<false>(x, x.P, s2, h * s2, Wss, C, CC, Q, s2, h * s2, h, s2, s2, 1.0, 0.0))
+    return rc;
+  if (int rc = factor_rec(x, b0, mid, depth + 1)) return rc;
+  // W_TS = -W_TT Q
+  return gemm<false>(x, x.W + r0 * C + r0, C, CC, Q, s2, h * s2, x.W + r0 * C + rm, C, CC, h, s2,
+                     h, -1.0, 0.0);
 }
 
 }  // namespace
@@ -289,7 +391,8 @@ __global__ void emit_u_kernel(const double* __restrict__ W, int64_t C,
 using namespace mgq;
 
 extern "C" int64_t mgq_hinv_full_workspace_size(int64_t B, int64_t C) {
-  return 2 * B * C * C * 8 + 256;
+  if (B < 0 || C < 1) return 0;
+  return make_layout(B, C).total;
 }
 
 // One factorisation pass for the items with active[b] != 0, using per-item
@@ -299,35 +402,31 @@ extern "C" int mgq_hinv_full_pass(const float* H, int64_t B, int64_t C, const fl
                                   void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   MGQ_REQUIRE(B >= 0 && C >= 1, MGQ_ERR_SHAPE, "bad shape");
-  MGQ_REQUIRE(workspace != nullptr && workspace_bytes >= mgq_hinv_full_workspace_size(B, C),
-              MGQ_ERR_WORKSPACE, "hinv workspace too small");
+  const Layout L = make_layout(B, C);
+  MGQ_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MGQ_ERR_WORKSPACE,
+              "hinv workspace too small");
   if (B == 0) return MGQ_OK;
   hipStream_t s = as_stream(stream);
-  double* A = static_cast<double*>(workspace);
-  double* W = A + B * C * C;
+  char* ws = static_cast<char*>(workspace);
+  Ctx x;
+  x.A = reinterpret_cast<double*>(ws);
+  x.W = x.A + B * C * C;
+  x.P = reinterpret_cast<double*>(ws + L.p_off);
+  for (int d = 0; d < 32; ++d) x.Q[d] = reinterpret_cast<double*>(ws + L.q_off[d]);
+  x.B = B;
+  x.C = C;
+  x.active = active;
+  x.failed = failed;
+  x.s = s;
+  float* lam = reinterpret_cast<float*>(ws + L.lam_off);
   const unsigned gb = static_cast<unsigned>(B);
-  build_hd_kernel<<<dim3(elementwise_blocks(C * C, 256) / 8 + 1, gb), 256, 0, s>>>(H, C, damp,
-                                                                                  active, A);
+  lam_kernel<<<gb, 256, 0, s>>>(H, C, damp, active, lam);
+  if (int rc = check_launch("hinv lam")) return rc;
+  build_kernel<<<dim3(std::min<unsigned>(elementwise_blocks(C * C, 256), 1024u), gb), 256, 0, s>>>(
+      H, C, lam, active, x.A, x.W);
   if (int rc = check_launch("hinv build")) return rc;
-  for (int64_t jb = ((C - 1) / kNb) * kNb; jb >= 0; jb -= kNb) {
-    const int n = static_cast<int>(std::min<int64_t>(kNb, C - jb));
-    diag_block_kernel<<<gb, 256, 0, s>>>(A, W, C, jb, n, active, failed);
-    if (int rc = check_launch("hinv diag")) return rc;
-    if (jb > 0) {
-      panel_kernel<<<dim3(static_cast<unsigned>(ceil_div(jb, 4)), gb), 256, 0, s>>>(A, W, C, jb, n,
-                                                                                   active, failed);
-      if (int rc = check_launch("hinv panel")) return rc;
-      const unsigned nt = static_cast<unsigned>(ceil_div(jb, kNb));
-      trailing_kernel<<<dim3(nt, nt, gb), 256, 0, s>>>(A, C, jb, n, active, failed);
-      if (int rc = check_launch("hinv trailing")) return rc;
-    }
-    if (jb + n < C) {
-      const unsigned mt = static_cast<unsigned>(ceil_div(C - jb - n, kNb));
-      wrow_kernel<<<dim3(mt, gb), 256, 0, s>>>(A, W, C, jb, n, active, failed);
-      if (int rc = check_launch("hinv wrow")) return rc;
-    }
-  }
-  emit_u_kernel<<<dim3(elementwise_blocks(C * C, 256) / 8 + 1, gb), 256, 0, s>>>(W, C, active,
-                                                                                failed, U);
+  if (int rc = factor_rec(x, 0, ceil_div(C, kNb), 0)) return rc;
+  emit_u_kernel<<<dim3(std::min<unsigned>(elementwise_blocks(C * C, 256), 1024u), gb), 256, 0, s>>>(
+      x.W, C, active, failed, U);
   return check_launch("hinv emit");
 }

@@ -113,3 +113,82 @@ def dense_linear(rows: int, cols: int, tokens: int, w_std: float = 0.02, sigma: 
     gw = torch.Generator(device=device).manual_seed(seed + 3000)
     W = (torch.randn(1, rows, cols, generator=gw, device=device) * w_std).to(torch.bfloat16)
     return W, X
+
+
+@torch.no_grad()
+def swiglu_inputs(n_tokens: int, channels: int, device, sigma: float = 1.0, seed: int = 29,
+                  chunk: int = 8192) -> torch.Tensor:
+    """Down-projection inputs bf16(SiLU(a) * b) with a, b ~ N(0, 1), each
+    channel scaled by exp(N(0, sigma)); chunk c uses generator seed + c."""
+    g = torch.Generator().manual_seed(seed - 1)
+    scale = torch.exp(torch.randn(channels, generator=g) * sigma).to(device)
+    out = torch.empty(n_tokens, channels, dtype=torch.bfloat16, device=device)
+    for c, a in enumerate(range(0, n_tokens, chunk)):
+        b = min(a + chunk, n_tokens)
+        gc = torch.Generator(device=device).manual_seed(seed + c)
+        x = torch.randn(b - a, channels, generator=gc, device=device)
+        y = torch.randn(b - a, channels, generator=gc, device=device)
+        out[a:b] = (F.silu(x) * y * scale).to(torch.bfloat16)
+        del x, y
+    return out
+
+
+@dataclass
+class DenseMatrix:
+    """One weight matrix of a dense layer and how the benchmark solves it."""
+
+    name: str
+    W: torch.Tensor   # bf16 [1, out, in]
+    inp: str          # key of its calibration input in DenseLayer.inputs
+    solve: dict       # solve_gptq keyword arguments (bits, group_size, mode, ...)
+    pack_bits: int
+
+
+@dataclass
+class DenseLayer:
+    name: str
+    inputs: dict      # key -> bf16 [tokens, in] calibration rows
+    mats: list        # DenseMatrix, in solve order
+
+    @property
+    def elements(self) -> int:
+        return sum(int(m.W.numel()) for m in self.mats)
+
+
+@torch.no_grad()
+def dense_config(cfg: int, device="cuda:0") -> DenseLayer:
+    """BASELINE configs 1, 2, 3 and 5 (dense linears / MLPs)."""
+    def w(rows, cols, std, seed):
+        gw = torch.Generator(device=device).manual_seed(seed)
+        return (torch.randn(1, rows, cols, generator=gw, device=device) * std).to(torch.bfloat16)
+
+    if cfg == 1:
+        X = _hidden_states(8192, 2048, device, outlier_frac=0.01, outlier_mult=20.0, seed=17)
+        return DenseLayer("cfg1 single Linear [2048,2048], affine 4-bit GPTQ (G=64, block 128, MSE clip)",
+                          {"x": X}, [DenseMatrix("linear", w(2048, 2048, 0.02, 3017), "x",
+                                                 dict(bits=4, group_size=64, mode="affine"), 4)])
+    if cfg == 2:
+        X = _hidden_states(32768, 4096, device, outlier_frac=0.005, outlier_mult=30.0, seed=17)
+        return DenseLayer("cfg2 Llama-3-8B q_proj [4096,4096], MXFP4 groupwise GPTQ",
+                          {"x": X}, [DenseMatrix("q_proj", w(4096, 4096, 0.02, 3017), "x",
+                                                 dict(bits=4, group_size=32, mode="mxfp4",
+                                                      mxfp_algorithm="groupwise"), 4)])
+    if cfg == 3:
+        X = _hidden_states(65536, 4096, device, outlier_frac=0.01, outlier_mult=20.0, seed=17)
+        Xd = swiglu_inputs(65536, 14336, device, seed=29)
+        kw = dict(bits=8, group_size=32, mode="mxfp8", mxfp_algorithm="groupwise")
+        return DenseLayer("cfg3 Llama-3-8B MLP: up [14336,4096] + down [4096,14336], MXFP8 groupwise GPTQ",
+                          {"x": X, "act": Xd},
+                          [DenseMatrix("up_proj", w(14336, 4096, 0.015, 3017), "x", kw, 8),
+                           DenseMatrix("down_proj", w(4096, 14336, 0.015, 3018), "act", kw, 8)])
+    if cfg == 5:
+        X = _hidden_states(524288, 5120, device, outlier_frac=0.01, outlier_mult=25.0, seed=17)
+        Xd = swiglu_inputs(524288, 25600, device, seed=29)
+        kw = dict(bits=4, group_size=32, mode="mxfp4", mxfp_algorithm="safe-scale-search")
+        return DenseLayer("cfg5 Qwen3-32B MLP: gate, up [25600,5120] + down [5120,25600], MXFP4 "
+                          "safe-scale-search GPTQ",
+                          {"x": X, "act": Xd},
+                          [DenseMatrix("gate_proj", w(25600, 5120, 0.015, 3017), "x", kw, 4),
+                           DenseMatrix("up_proj", w(25600, 5120, 0.015, 3018), "x", kw, 4),
+                           DenseMatrix("down_proj", w(5120, 25600, 0.015, 3019), "act", kw, 4)])
+    raise ValueError(f"no dense benchmark config {cfg} (1, 2, 3 or 5; config 4 is moe_layer)")
