@@ -175,9 +175,9 @@ def run_moe(args, torch, np) -> int:
     _copy_calibration(torch, dev, args.copy_calib_mib)
     out, ms_step, phase = _timed(torch, np, step, 5, args.warmup, args.steps)
     value = elements / (ms_step * 1e-3)
-    roofline = _roofline("syrk_dma_kernel (gate_up Hessian, routed gather)", "mfma",
+    roofline = _roofline("syrk_kernel (gate_up Hessian, routed gather)", "mfma",
                          A * hidden * (hidden + 1),  # SYRK count N*C*(C+1)
-                         float(phase[0]), _traffic("bench_moe_cfg4", "mgq::syrk_dma_kernel<true>"))
+                         float(phase[0]), _traffic("bench_moe_cfg4", "mgq::syrk_kernel<true"))
     cpu = _cpu_baseline_moe(L, ne, out, args.cpu_seconds) if args.cpu_seconds > 0 else None
     config = {
         "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
@@ -279,7 +279,7 @@ def run_dense(args, torch, np) -> int:
     for i, k in enumerate(keys):
         N, C = L.inputs[k].shape
         phases[f"hessian_{k}"] = phase[i]
-        rooflines[f"hessian_{k}"] = _roofline(f"syrk_dma_kernel (Hessian of '{k}', [{N}x{C}])", "mfma",
+        rooflines[f"hessian_{k}"] = _roofline(f"syrk_kernel (Hessian of '{k}', [{N}x{C}])", "mfma",
                                               N * C * (C + 1), float(phase[i]))
     for j, m in enumerate(L.mats):
         ms = float(phase[len(keys) + j])
@@ -295,7 +295,7 @@ def run_dense(args, torch, np) -> int:
     dom = max(rooflines, key=lambda k: rooflines[k]["launch_ms"])
     if dom.startswith("hessian_"):
         # the profile's largest SYRK dispatch is the dominant Hessian
-        rooflines[dom]["traffic"] = _traffic(tag, "mgq::syrk_dma_kernel<false>")
+        rooflines[dom]["traffic"] = _traffic(tag, "mgq::syrk_kernel<false")
     cpu = _cpu_baseline_dense(L, out, Hs, args.cpu_seconds) if args.cpu_seconds > 0 else None
     config = {"workload": L.name, "elements": elements,
               "matrices": {m.name: list(m.W.shape[1:]) for m in L.mats},

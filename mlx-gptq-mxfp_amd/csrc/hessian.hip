@@ -11,18 +11,17 @@
 // Tile kernel (256 threads = 4 waves, 1 workgroup per CU):
 //   - output tile 256x256, each wave 128x128 = 4x4 blocks of
 //     v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, in AGPRs);
-//   - token rows are copied HBM -> LDS by global_load_lds_dwordx4 with a
-//     scalar (SGPR) row address per token, so the gather costs no vector
-//     work; MFMA operands are read with ds_read_b64_tr_b16 transposing loads
-//     from the token-major LDS rows (see syrk_dma_kernel);
+//   - token rows are copied HBM -> LDS by global_load_lds_dwordx4 (no VGPR
+//     staging); MFMA operands are read with ds_read_b64_tr_b16 transposing
+//     loads from the token-major LDS rows (see syrk_kernel);
+//   - one MFMA at a time is interleaved with the other work of its K-step
+//     (one LDS fragment read, the next stage's DMA, address arithmetic), so
+//     the matrix pipe never waits for a burst of non-MFMA instructions;
 //   - one work item accumulates at most 262144 tokens in the MFMA fp32
 //     accumulators (longer token ranges are split into partial tiles), which
 //     bounds the accumulation chain well inside the 1e-5 Frobenius budget.
-// Work items are planned on the host (mgq_hessian_plan): groups are spread
-// over the 8 XCDs by token load (LPT) and all tiles of a group stay on one
-// XCD so its token rows are shared through that XCD's L2. Heavy groups are
-// split along K into partial tiles summed in a fixed order by a second
-// kernel, keeping H deterministic.
+// Work items are planned on the host (mgq_hessian_plan), see build_plan.
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -43,6 +42,7 @@ constexpr int kKs = 64;          // token granularity of work-item ranges
 constexpr int kThreads = 256;
 constexpr int64_t kMaxItemTokens = 262144;  // longest fp32 accumulation chain per item
 constexpr int kXcds = 8;
+constexpr int kCUs = 256;
 
 struct HessItem {
   int32_t g;     // group, -1 = no-op padding
@@ -141,77 +141,50 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS SYRK (production kernel).
+// SYRK tile kernel.
 //
-// Token rows go from HBM straight into LDS with global_load_lds_dwordx4 (no
-// VGPR staging, no register transpose): one instruction moves one token's
-// 256 A channels (lanes 0-31) and 256 B channels (lanes 32-63), 1 KB, with
-// a 64-bit SGPR row address, so the routed gather costs scalar work only.
-// LDS keeps token-major rows (as in HBM); MFMA operands (one channel x 8
-// consecutive tokens per lane) come out of ds_read_b64_tr_b16, which hands
-// lane i of each 16-lane group element i%4 of source lanes 4j + i/4, j=0..3:
-// pointing source lane 4j+q at token j, channels 4q..4q+3 gives lane i
-// channel i of tokens 0..3. Four 32-token stages are in flight; each wave
-// waits for its own DMA of a stage (vmcnt) before the stage barrier. The
-// 16-byte chunk index of LDS token row t is XORed with 4*(t & 3), so the 64
-// bytes a transposed read takes from each of its 8 token rows land on four
-// distinct 64-byte bank groups (two LDS cycles per read, no conflicts).
-constexpr int kTokB = 1024;  // LDS bytes per token: A row | B row
-#ifndef MGQ_SYRK_KB
-#define MGQ_SYRK_KB 64  // tokens per LDS stage (one barrier each)
-#endif
-#ifndef MGQ_SYRK_NB
-#define MGQ_SYRK_NB 2   // stage buffers (NB - 1 stages of DMA in flight)
-#endif
-constexpr int kDK = MGQ_SYRK_KB;
-constexpr int kDBuf = MGQ_SYRK_NB;
-constexpr int kStageB = kDK * kTokB;
-constexpr int kDmaWave = kDK / 4;  // tokens (= DMA instructions) per wave and stage
-static_assert(kDBuf * kStageB <= 160 * 1024, "LDS budget");
-static_assert((kDBuf - 2) * kDmaWave <= 63, "vmcnt range");
+// LDS holds NB stages of KB tokens; token row t of a stage is 1 KB: the 256
+// A channels, then the 256 B channels of the tile (diagonal tiles load the A
+// channels into both halves). One global_load_lds_dwordx4 moves one token
+// row (lanes 0-31 the A half, 32-63 the B half) straight from HBM into LDS.
+// Its address is saddr (SGPR pair) + a 32-bit VGPR offset:
+//   - dense: saddr = the stage's first row of this wave, offset = lane chunk
+//     + i * row pitch (fixed per lane);
+//   - gathered, X < 4 GB: saddr = X, offset = row_index[t] * pitch + lane
+//     chunk (one v_readlane + multiply-add per token; the wave's 16 indices
+//     of a stage arrive in one vector load two stages ahead);
+//   - gathered, X >= 4 GB (BIG): saddr = X + row * pitch per token.
+// Tokens past the item's range read a zero row.
+//
+// MFMA operands (one channel x 8 consecutive tokens per lane) come from
+// ds_read_b64_tr_b16, which hands lane i of each 16-lane group element i%4
+// of source lanes 4j + i/4, j=0..3: pointing source lane 4j+q at token j,
+// channels 4q..4q+3 gives lane i channel i of tokens 0..3. The 16-byte chunk
+// index of LDS token row t is XORed with 4*(t & 3), so the 64 bytes a
+// transposed read takes from each of its 8 token rows land on four distinct
+// 64-byte bank groups (no conflicts).
+//
+// Schedule of one stage s (nks = KB/16 K-steps of 16 MFMAs, 4x4 blocks of
+// the wave's 128x128 tile): segment k (k = 1..nks-1) runs the 16 MFMAs of
+// K-step k-1, each followed by its share of the fragment reads of K-step k.
+// Then the stage barrier (this wave's DMA of stage s+1 done: vmcnt; every
+// wave done reading stage s: lgkmcnt(0) before s_barrier), after which
+// segment 0 of stage s+1 runs the last K-step's MFMAs of stage s together
+// with the first fragment reads of stage s+1 and the DMA of stage s+NB into
+// the buffer stage s just released. Fragments are double-buffered in VGPRs
+// (fa/fb[2][4]); each MFMA is fenced by sched_barrier so this order is kept.
+__device__ inline void dma_tok(uint32_t lds_dst, uint32_t voffset, const char* saddr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_dst), "v"(voffset), "s"(saddr)
+               : "memory", "m0");
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 typedef __attribute__((address_space(3))) char lds_char_t;
-
-__device__ inline void dma_row(uint32_t lds_dst, uint32_t voff, const void* saddr) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_dst), "v"(voff), "s"(saddr)
-               : "memory");
-}
-
-// Wait until at most N of this wave's DMA loads are outstanding and its LDS
-// reads / scalar loads are done, then barrier.
-template <int N>
-__device__ inline void stage_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "i"(N) : "memory");
-}
-
-// `ahead` stages of DMA (kDmaWave loads each) were issued after the stage
-// being waited for; the count is an immediate, so dispatch on it.
-__device__ inline void stage_barrier_ahead(int ahead) {
-  if constexpr (kDBuf - 2 >= 3) {
-    if (ahead >= 3) {
-      stage_barrier<3 * kDmaWave>();
-      return;
-    }
-  }
-  if constexpr (kDBuf - 2 >= 2) {
-    if (ahead >= 2) {
-      stage_barrier<2 * kDmaWave>();
-      return;
-    }
-  }
-  if constexpr (kDBuf - 2 >= 1) {
-    if (ahead >= 1) {
-      stage_barrier<kDmaWave>();
-      return;
-    }
-  }
-  stage_barrier<0>();
-}
+constexpr int kTokB = 1024;  // LDS bytes per token: A row | B row
 
 __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
@@ -220,37 +193,39 @@ __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-template <bool GATHER>
-__device__ inline void stage_rows(const char* __restrict__ Xb, uint32_t ldx2, uint32_t n_rows,
-                                  const int32_t* __restrict__ row_index, int64_t t0, int64_t k1,
-                                  const char* zero_row, const char* (&src)[kDmaWave]) {
-#pragma unroll
-  for (int i = 0; i < kDmaWave; ++i) {
-    const int64_t t = t0 + i;
-    uint32_t row;
-    if (GATHER) {
-      const uint32_t r = static_cast<uint32_t>(row_index[t < k1 ? t : k1 - 1]);
-      row = r < n_rows ? r : n_rows - 1;
-    } else {
-      row = static_cast<uint32_t>(t < k1 ? t : k1 - 1);
-    }
-    src[i] = t < k1 ? Xb + static_cast<uint64_t>(row) * ldx2 : zero_row;
-  }
-}
+#define SYRK_MFMA(P, j)                                                                    \
+  acc[(j) >> 2][(j) & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                        \
+      fa[P][(j) >> 2], fb[P][(j) & 3], acc[(j) >> 2][(j) & 3], 0, 0, 0)
+// fragment q of a K-step, in the order the MFMAs consume them: a0 b0 b1 b2 b3 a1 a2 a3
+#define SYRK_READ(P, q, b)                                                                 \
+  do {                                                                                     \
+    if ((q) == 0)                                                                          \
+      fa[P][0] = tr_frag(lds3 + (b) + offA[0]);                                            \
+    else if ((q) <= 4)                                                                     \
+      fb[P][(q) - 1] = tr_frag(lds3 + (b) + offB[(q) - 1]);                                \
+    else                                                                                   \
+      fa[P][(q) - 4] = tr_frag(lds3 + (b) + offA[(q) - 4]);                                \
+  } while (0)
 
-__device__ inline void issue_stage(uint32_t dst, const uint32_t (&voff)[4],
-                                   const char* const (&src)[kDmaWave]) {
-#pragma unroll
-  for (int i = 0; i < kDmaWave; ++i) dma_row(dst + i * kTokB, voff[i & 3], src[i]);
-}
-
-template <bool GATHER>
+template <bool GATHER, bool BIG, int KB, int NB>
 __global__ void __launch_bounds__(kThreads, 1)
-    syrk_dma_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
-                    const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
-                    float* __restrict__ H, float* __restrict__ partials, int accumulate,
-                    const uint16_t* __restrict__ zero_row) {
-  __shared__ __attribute__((aligned(1024))) char lds[kDBuf * kStageB];
+    syrk_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
+                const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
+                float* __restrict__ H, float* __restrict__ partials, int accumulate,
+                const uint16_t* __restrict__ zero_row) {
+  constexpr int kDmaWave = KB / 4;  // tokens (= DMA instructions) per wave and stage
+  constexpr int kStageB = KB * kTokB;
+  constexpr int nks = KB / 16;
+  constexpr int L = (nks - 1) & 1;  // fragment buffer of a stage's last K-step
+  constexpr int kDmaEvery = 16 / kDmaWave;
+  static_assert(KB % 32 == 0 && kDmaWave <= 16, "stage shape");
+  static_assert(NB * kStageB <= 160 * 1024, "LDS budget");
+  static_assert(!GATHER || NB == 2, "gathered row indices are loaded one stage ahead");
+  // stage barrier: vmcnt(DMA stages still allowed in flight), lgkmcnt(0)
+  constexpr int kVm = (NB - 2) * kDmaWave;
+  static_assert(kVm <= 63, "vmcnt range");
+  constexpr int kWait = (kVm & 15) | ((kVm >> 4) << 14) | (7 << 4);
+  __shared__ __attribute__((aligned(1024))) char lds[NB * kStageB];
 
   const HessItem it = items[blockIdx.x];
   if (it.g < 0) return;
@@ -268,8 +243,7 @@ __global__ void __launch_bounds__(kThreads, 1)
 
   // DMA lane role: slot (lane & 31) of the A (lane < 32) or B half of LDS
   // token row t holds chunk slot ^ 4*(t & 3); channels past C are clamped (they
-  // only feed output rows / columns >= C, which are never stored). Diagonal
-  // tiles load the A channels into both halves.
+  // only feed output rows / columns >= C, which are never stored).
   const int half = lane >> 5;
   const int64_t tile_ch = static_cast<int64_t>(half && !diag ? it.tj : it.ti) * kTile;
   uint32_t voff[4];
@@ -280,14 +254,14 @@ __global__ void __launch_bounds__(kThreads, 1)
   }
   // Transposed-read lane role: group g = lane/16, source j = (lane/4)%4, q = lane%4.
   // Source j reads LDS token row 4r + j (+ 8, 16 multiples), so its swizzle is j.
-  const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
-  const uint32_t rd_lo = static_cast<uint32_t>((8 * (g >> 1) + j) * kTokB + (g & 1) * 32 +
+  const int g = lane >> 4, j4 = (lane >> 2) & 3, q = lane & 3;
+  const uint32_t rd_lo = static_cast<uint32_t>((8 * (g >> 1) + j4) * kTokB + (g & 1) * 32 +
                                                (q >> 1) * 16 + (q & 1) * 8);
   uint32_t offA[4], offB[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    offA[m] = rd_lo + wr * 256 + (m ^ j) * 64;
-    offB[m] = rd_lo + 512 + wc * 256 + (m ^ j) * 64;
+    offA[m] = rd_lo + wr * 256 + (m ^ j4) * 64;
+    offB[m] = rd_lo + 512 + wc * 256 + (m ^ j4) * 64;
   }
   const lds_char_t* lds3 = (const lds_char_t*)lds;
   const uint32_t lds_u32 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds3));
@@ -304,62 +278,130 @@ __global__ void __launch_bounds__(kThreads, 1)
   const char* Xb = reinterpret_cast<const char*>(X);
   const char* zr = reinterpret_cast<const char*>(zero_row);
   const uint32_t ldx2 = static_cast<uint32_t>(2 * ldx);
-  const uint32_t nr = static_cast<uint32_t>(n_rows);
+  const uint32_t nr1 = static_cast<uint32_t>(n_rows - 1);
   const int64_t k0 = it.k0, k1 = it.k1;
-  const int n_stages = static_cast<int>((k1 - k0 + kDK - 1) / kDK);
+  const int n_stages = static_cast<int>((k1 - k0 + KB - 1) / KB);
   const int64_t twave = k0 + wave * kDmaWave;  // this wave's first token of stage 0
-
-  const char* src[kDmaWave];
-  // prologue: stages 0 .. kDBuf-2 in flight
+  uint32_t vofs[kDmaWave];
 #pragma unroll
-  for (int p = 0; p < kDBuf - 1; ++p) {
-    if (p < n_stages) {
-      stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + p * kDK, k1, zr, src);
-      issue_stage(lds_u32 + p * kStageB + wave_dst, voff, src);
+  for (int i = 0; i < kDmaWave; ++i) vofs[i] = voff[i & 3] + i * ldx2;
+
+  // Row indices of this wave's tokens of the stage starting at t0: lane i
+  // (i < kDmaWave) holds token t0 + i, clamped into the item's range.
+  auto load_idx = [&](int64_t t0) -> int32_t {
+    if constexpr (GATHER) {
+      const int64_t t = t0 + (lane & (kDmaWave - 1));
+      return row_index[t < k1 ? t : k1 - 1];
+    } else {
+      return 0;
     }
-  }
-  if (kDBuf - 1 < n_stages)
-    stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + (kDBuf - 1) * kDK, k1, zr, src);
+  };
+  // DMA of token i of this wave's share of a stage (rem tokens are in range).
+  auto dma_i = [&](int i, uint32_t dst, int rem, int32_t idxv, const char* base) {
+    const char* sa;
+    uint32_t vo;
+    if constexpr (GATHER) {
+      uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(idxv, i));
+      r = r < nr1 ? r : nr1;  // a bad index is clamped, never dereferenced
+      if constexpr (BIG) {
+        sa = Xb + static_cast<uint64_t>(r) * ldx2;
+        vo = voff[i & 3];
+      } else {
+        sa = Xb;
+        vo = r * ldx2 + voff[i & 3];
+      }
+    } else {
+      sa = base;
+      vo = vofs[i];
+    }
+    const bool ok = i < rem;
+    dma_tok(dst + i * kTokB, ok ? vo : voff[i & 3], ok ? sa : zr);
+  };
+  auto stage_rem = [&](int64_t t0) -> int {
+    const int64_t r = k1 - t0;
+    return static_cast<int>(r < 0 ? 0 : (r > kDmaWave ? kDmaWave : r));
+  };
+  auto stage_base = [&](int64_t t0) -> const char* {
+    return Xb + static_cast<uint64_t>(t0 < k1 ? t0 : k0) * ldx2;
+  };
 
-  int rbuf = 0, wbuf = kDBuf - 1;  // buffer of stage s, buffer of stage s + kDBuf - 1
-  for (int s = 0; s < n_stages; ++s) {
-    stage_barrier_ahead(n_stages - 1 - s);
-    const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
+  if (n_stages > 0) {
     bf16x8_t fa[2][4], fb[2][4];
+    // prologue: stages 0 .. NB-2 in flight, barrier, first fragments, stage NB-1
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      fa[0][m] = tr_frag(lds3 + rd + offA[m]);
-      fb[0][m] = tr_frag(lds3 + rd + offB[m]);
+    for (int p = 0; p < NB - 1; ++p) {
+      const int64_t t0 = twave + p * KB;
+      const int32_t idx0 = load_idx(t0);
+      const int rem = stage_rem(t0);
+      const char* base = stage_base(t0);
+#pragma unroll
+      for (int i = 0; i < kDmaWave; ++i) dma_i(i, lds_u32 + p * kStageB + wave_dst, rem, idx0, base);
+    }
+    int32_t idx_n = load_idx(twave + (NB - 1) * KB);
+    __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int qq = 0; qq < 8; ++qq) SYRK_READ(0, qq, 0u);
+    {
+      // stages past the item's range load zero rows (their buffers are never read)
+      const int64_t t0 = twave + (NB - 1) * KB;
+      const int rem = stage_rem(t0);
+      const char* base = stage_base(t0);
+#pragma unroll
+      for (int i = 0; i < kDmaWave; ++i)
+        dma_i(i, lds_u32 + (NB - 1) * kStageB + wave_dst, rem, idx_n, base);
     }
     __builtin_amdgcn_sched_barrier(0);
+    int rbuf = 0;
+    for (int s = 0; s < n_stages - 1; ++s) {
+      const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
 #pragma unroll
-    for (int ks = 0; ks < kDK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < kDK / 16) {
+      for (int ks = 1; ks < nks; ++ks) {
+        const int P = (ks - 1) & 1;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          fa[cur ^ 1][m] = tr_frag(lds3 + rd + offA[m] + (ks + 1) * 16 * kTokB);
-          fb[cur ^ 1][m] = tr_frag(lds3 + rd + offB[m] + (ks + 1) * 16 * kTokB);
+        for (int j = 0; j < 16; ++j) {
+          SYRK_MFMA(P, j);
+          if ((j & 1) == 0) SYRK_READ(P ^ 1, j >> 1, rd + ks * 16 * kTokB);
+          if (GATHER && ks == 1 && j == 1)
+            idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      if (ks == 0 && s + kDBuf - 1 < n_stages) {
-        // the buffer of stage s-1: every wave finished it before the barrier
-        issue_stage(lds_u32 + wbuf * kStageB + wave_dst, voff, src);
+      const uint32_t wbuf = static_cast<uint32_t>(rbuf);  // stage s's buffer takes stage s+NB
+      rbuf = rbuf + 1 == NB ? 0 : rbuf + 1;
+      __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t nrd = static_cast<uint32_t>(rbuf * kStageB);
+      const uint32_t dst = lds_u32 + wbuf * kStageB + wave_dst;
+      const int64_t t0 = twave + static_cast<int64_t>(s + NB) * KB;
+      const int rem = stage_rem(t0);
+      const char* base = stage_base(t0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        SYRK_MFMA(L, j);
+        if ((j & 1) == 0) SYRK_READ(L ^ 1, j >> 1, nrd);
+        if (j % kDmaEvery == kDmaEvery - 1) dma_i(j / kDmaEvery, dst, rem, idx_n, base);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ma = 0; ma < 4; ++ma)
-#pragma unroll
-        for (int na = 0; na < 4; ++na)
-          acc[ma][na] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][ma], fb[cur][na],
-                                                                acc[ma][na], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
     }
-    if (s + kDBuf < n_stages)
-      stage_rows<GATHER>(Xb, ldx2, nr, row_index, twave + static_cast<int64_t>(s + kDBuf) * kDK,
-                         k1, zr, src);
-    rbuf = rbuf + 1 == kDBuf ? 0 : rbuf + 1;
-    wbuf = wbuf + 1 == kDBuf ? 0 : wbuf + 1;
+    {
+      const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
+#pragma unroll
+      for (int ks = 1; ks < nks; ++ks) {
+        const int P = (ks - 1) & 1;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          SYRK_MFMA(P, j);
+          if ((j & 1) == 0) SYRK_READ(P ^ 1, j >> 1, rd + ks * 16 * kTokB);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) SYRK_MFMA(L, j);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the trailing (zero-row) stages' DMA
   }
   // Empty ranges (n_stages == 0) still flush, so an unrouted group gets H = 0.
   const bool interior =
@@ -367,6 +409,8 @@ __global__ void __launch_bounds__(kThreads, 1)
   flush(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
         interior);
 }
+#undef SYRK_MFMA
+#undef SYRK_READ
 
 __global__ void zero_fill_kernel(uint32_t* __restrict__ p, int64_t n_words) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_words;
@@ -375,30 +419,65 @@ __global__ void zero_fill_kernel(uint32_t* __restrict__ p, int64_t n_words) {
 }
 
 // Sum the K-split partial tiles of one output tile in slot order and write
-// the lower triangle (+ mirror) of H.
-__global__ void reduce_split_kernel(const SplitTile* __restrict__ tiles,
-                                    const float* __restrict__ partials, float* __restrict__ H,
-                                    int64_t C, int accumulate) {
+// the lower triangle (+ mirror) of H. One block per 64x64 sub-tile: partial
+// rows are read and H rows written along the fast index, and the mirrored
+// values go out through an LDS transpose, so both stores are coalesced.
+constexpr int kRedSub = 64;
+__global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __restrict__ tiles,
+                                                           const float* __restrict__ partials,
+                                                           float* __restrict__ H, int64_t C,
+                                                           int accumulate) {
+  __shared__ float tr[kRedSub][kRedSub + 1];
   const SplitTile st = tiles[blockIdx.y];
   float* Hg = H + static_cast<int64_t>(st.g) * C * C;
-  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < kTile * kTile;
-       e += gridDim.x * blockDim.x) {
-    const int li = e / kTile, lj = e % kTile;
-    const int64_t gi = static_cast<int64_t>(st.ti) * kTile + li;
-    const int64_t gj = static_cast<int64_t>(st.tj) * kTile + lj;
-    if (gi >= C || gj >= C || gi < gj) continue;
-    float v = partials[static_cast<int64_t>(st.slot0) * kTile * kTile + e];
-    for (int s = 1; s < st.nslots; ++s)
-      v += partials[static_cast<int64_t>(st.slot0 + s) * kTile * kTile + e];
-    float* p = Hg + gi * C + gj;
-    const float nv = accumulate ? (*p + v) : v;
-    *p = nv;
-    if (gi != gj) Hg[gj * C + gi] = nv;
+  const int sr = blockIdx.x / (kTile / kRedSub), sc = blockIdx.x % (kTile / kRedSub);
+  const int64_t bi = static_cast<int64_t>(st.ti) * kTile + sr * kRedSub;  // global row base
+  const int64_t bj = static_cast<int64_t>(st.tj) * kTile + sc * kRedSub;  // global column base
+  const int c = threadIdx.x & (kRedSub - 1), r0 = threadIdx.x / kRedSub;
+  const float* p0 = partials + static_cast<int64_t>(st.slot0) * kTile * kTile;
+#pragma unroll 4
+  for (int r = r0; r < kRedSub; r += 256 / kRedSub) {
+    const int e = (sr * kRedSub + r) * kTile + sc * kRedSub + c;
+    float v = p0[e];
+    for (int s = 1; s < st.nslots; ++s) v += p0[static_cast<int64_t>(s) * kTile * kTile + e];
+    const int64_t gi = bi + r, gj = bj + c;
+    float nv = v;
+    if (gi < C && gj < C && gi >= gj) {
+      float* p = Hg + gi * C + gj;
+      nv = accumulate ? (*p + v) : v;
+      *p = nv;
+    }
+    tr[c][r] = nv;
+  }
+  __syncthreads();
+  // mirror: H[bj + r][bi + c] = value of (bi + c, bj + r), strictly below the diagonal
+#pragma unroll 4
+  for (int r = r0; r < kRedSub; r += 256 / kRedSub) {
+    const int64_t gi = bi + c, gj = bj + r;
+    if (gi < C && gj < C && gi > gj) Hg[gj * C + gi] = tr[r][c];
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host planning.
+//
+// The hardware hands workgroup i to XCD i mod 8, and each XCD (32 CUs) has
+// its own L2; token rows fetched by one tile are reused from that L2 by the
+// other tiles that read the same channel blocks at about the same time. So:
+//   - tiles are enumerated in 4x4 super-block order of the lower triangle,
+//     and the work items of a group are laid out split-major (all tiles of
+//     token chunk 0, then chunk 1, ...): the ~32 items an XCD runs together
+//     share one token range and touch few channel blocks;
+//   - a group's item list is cut into at most 8 contiguous runs (>= 32 items)
+//     that go to the least-loaded XCD, heaviest first (LPT), and the XCD
+//     queues are interleaved into the grid;
+//   - K splits: every item covers at most kMaxItemTokens tokens; when the
+//     launch has few tile items (one dense layer), the token range is split
+//     further to fill the 256 CUs, choosing the split count by a cost model
+//     (rounds of 256 items x tokens per item, plus the partial-tile traffic).
+//     Partial tiles are summed in a fixed order by reduce_split_kernel, so H
+//     is deterministic. target_items > 0 instead sets the split directly
+//     (chunk = max(2048, tokens*tiles/target_items)).
 // ---------------------------------------------------------------------------
 struct Plan {
   PlanHeader hdr;
@@ -406,34 +485,55 @@ struct Plan {
   std::vector<SplitTile> split;
 };
 
+std::vector<std::pair<int32_t, int32_t>> blocked_tiles(int64_t nt) {
+  constexpr int64_t SB = 4;
+  std::vector<std::pair<int32_t, int32_t>> t;
+  const int64_t nsb = ceil_div(nt, SB);
+  for (int64_t I = 0; I < nsb; ++I)
+    for (int64_t J = 0; J <= I; ++J)
+      for (int64_t i = SB * I; i < std::min(nt, SB * I + SB); ++i)
+        for (int64_t j = SB * J; j < std::min(nt, SB * J + SB); ++j)
+          if (j <= i) t.emplace_back(static_cast<int32_t>(i), static_cast<int32_t>(j));
+  return t;
+}
+
 int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t target_items,
                Plan* plan) {
   const int64_t nt = ceil_div(C, kTile);
-  const int64_t T = nt * (nt + 1) / 2;
-  std::vector<std::pair<int32_t, int32_t>> tiles;
-  tiles.reserve(T);
-  for (int32_t i = 0; i < nt; ++i)
-    for (int32_t j = 0; j <= i; ++j) tiles.emplace_back(i, j);
-
-  int64_t total_tokens = 0;
+  const auto tiles = blocked_tiles(nt);
+  const int64_t T = static_cast<int64_t>(tiles.size());
+  int64_t active = 0, n_max = 0, total_tokens = 0;
   for (int64_t g = 0; g < n_groups; ++g) {
     const int64_t n = offsets[g + 1] - offsets[g];
     MGQ_REQUIRE(n >= 0, MGQ_ERR_SHAPE, "offsets must be non-decreasing (group %lld)",
                 (long long)g);
+    if (n > 0) ++active;
+    n_max = std::max(n_max, n);
     total_tokens += n;
   }
-  if (target_items <= 0) target_items = 4 * 256;
-  // K chunk per work item: balance the grid, never below 2048 tokens.
-  const int64_t work = std::max<int64_t>(total_tokens, 1) * T;
-  int64_t chunk = std::max<int64_t>(2048, ceil_div(work, target_items));
-  chunk = std::min<int64_t>(chunk, kMaxItemTokens);
-  chunk = ceil_div(chunk, kKs) * kKs;
+  // tokens per item: explicit (target_items > 0) or from the cost model
+  int64_t s_bal = 1, chunk_explicit = 0;
+  if (target_items > 0) {
+    const int64_t work = std::max<int64_t>(total_tokens, 1) * T;
+    chunk_explicit = std::max<int64_t>(2048, ceil_div(work, target_items));
+  } else {
+    const int64_t base = active * T;
+    if (base > 0 && base < 8 * kCUs) {
+      double best = 1e300;
+      for (int64_t sv = 1; sv <= 16; ++sv) {
+        const int64_t per = ceil_div(ceil_div(n_max, sv), kKs) * kKs;
+        if (sv > 1 && per < 512) break;
+        // 40 ns per token per 256x256 tile item, 100 ns per partial tile
+        const double cost = static_cast<double>(ceil_div(base * sv, kCUs)) * per * 40e-9 +
+                            (sv > 1 ? static_cast<double>(base * sv) * 100e-9 : 0.0);
+        if (cost < best * 0.98) {
+          best = cost;
+          s_bal = sv;
+        }
+      }
+    }
+  }
 
-  // Work units: a group's items (tiles x K splits) in tile order, cut into at
-  // most 8 contiguous chunks of >= 32 items (one XCD has 32 CUs). Small groups
-  // (one expert) stay whole on one XCD so their token rows are reused from
-  // that XCD's L2; big dense groups spread over all XCDs. Chunks go to the
-  // least-loaded XCD, heaviest first (LPT).
   struct Chunk {
     int64_t work;
     std::vector<HessItem> items;
@@ -443,21 +543,37 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
   for (int64_t g = 0; g < n_groups; ++g) {
     const int64_t k0 = offsets[g], k1 = offsets[g + 1];
     const int64_t n = k1 - k0;
-    const int64_t S = std::max<int64_t>(1, ceil_div(n, chunk));
-    const int64_t per = ceil_div(ceil_div(std::max<int64_t>(n, 1), S), kKs) * kKs;
+    int64_t per;
+    if (n == 0) {
+      per = 1;
+    } else if (chunk_explicit > 0) {
+      per = std::min<int64_t>(chunk_explicit, kMaxItemTokens);
+    } else {
+      const int64_t S = std::max<int64_t>(ceil_div(n, kMaxItemTokens), s_bal);
+      per = ceil_div(n, S);
+    }
+    per = ceil_div(per, kKs) * kKs;
+    const int64_t S = n == 0 ? 1 : ceil_div(n, per);  // chunks actually used
     std::vector<HessItem> gi;
-    for (const auto& t : tiles) {
-      if (S == 1) {
+    gi.reserve(T * S);
+    if (S == 1) {
+      for (const auto& t : tiles)
         gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second, -1, k0, k1});
-      } else {
-        const int32_t slot0 = static_cast<int32_t>(n_slots);
-        int32_t ns = 0;
-        for (int64_t a = k0; a < k1; a += per, ++ns) {
-          gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second,
-                                static_cast<int32_t>(n_slots++), a, std::min(a + per, k1)});
-        }
-        plan->split.push_back(SplitTile{static_cast<int32_t>(g), t.first, t.second, slot0, ns, 0});
+    } else {
+      const int64_t slot_base = n_slots;
+      for (int64_t c = 0; c < S; ++c) {
+        const int64_t a = k0 + c * per;
+        for (int64_t ti = 0; ti < T; ++ti)
+          gi.push_back(HessItem{static_cast<int32_t>(g), tiles[ti].first, tiles[ti].second,
+                                static_cast<int32_t>(slot_base + ti * S + c), a,
+                                std::min(a + per, k1)});
       }
+      for (int64_t ti = 0; ti < T; ++ti)
+        plan->split.push_back(SplitTile{static_cast<int32_t>(g), tiles[ti].first,
+                                        tiles[ti].second,
+                                        static_cast<int32_t>(slot_base + ti * S),
+                                        static_cast<int32_t>(S), 0});
+      n_slots += T * S;
     }
     const int64_t n_items = static_cast<int64_t>(gi.size());
     const int64_t parts = std::min<int64_t>(kXcds, std::max<int64_t>(1, n_items / 32));
@@ -470,6 +586,7 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
       chunks.push_back(std::move(c));
     }
   }
+  MGQ_REQUIRE(n_slots < (int64_t(1) << 31), MGQ_ERR_SHAPE, "hessian plan: too many partial tiles");
   std::stable_sort(chunks.begin(), chunks.end(),
                    [](const Chunk& a, const Chunk& b) { return a.work > b.work; });
   std::vector<std::vector<HessItem>> bins(kXcds);
@@ -499,6 +616,14 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
   h.plan_bytes = align_up(h.split_off + h.n_split * static_cast<int64_t>(sizeof(SplitTile)));
   h.k_end_max = offsets[n_groups];
   return MGQ_OK;
+}
+
+// Gathered launches use the 32-bit row-offset form when every row of X is
+// addressable with a 32-bit offset from X; MGQ_HESSIAN_WIDE_ADDR=1 forces the
+// 64-bit per-token form (used to test it on small inputs).
+bool wide_gather_addr(int64_t n_rows, int64_t ldx) {
+  const char* e = getenv("MGQ_HESSIAN_WIDE_ADDR");
+  return (e != nullptr && e[0] == '1') || n_rows * ldx * 2 + 16 > (int64_t(1) << 32);
 }
 
 }  // namespace
@@ -563,19 +688,22 @@ extern "C" int mgq_hessian(const void* X, int64_t n_rows, int64_t ldx, int64_t C
   if (h.n_items > 0) {
     zero_fill_kernel<<<1, 256, 0, s>>>(reinterpret_cast<uint32_t*>(zero_row), zbytes / 4);
     if (int rc = check_launch("hessian zero row")) return rc;
-    if (row_index) {
-      syrk_dma_kernel<true><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
-          static_cast<const uint16_t*>(X), n_rows, ldx, C, row_index, items, H, partials,
-          accumulate, zero_row);
+    const dim3 grid(static_cast<unsigned>(h.n_items));
+    const uint16_t* Xh = static_cast<const uint16_t*>(X);
+    if (row_index && wide_gather_addr(n_rows, ldx)) {
+      syrk_kernel<true, true, 64, 2><<<grid, kThreads, 0, s>>>(
+          Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
+    } else if (row_index) {
+      syrk_kernel<true, false, 64, 2><<<grid, kThreads, 0, s>>>(
+          Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
     } else {
-      syrk_dma_kernel<false><<<static_cast<unsigned>(h.n_items), kThreads, 0, s>>>(
-          static_cast<const uint16_t*>(X), n_rows, ldx, C, nullptr, items, H, partials,
-          accumulate, zero_row);
+      syrk_kernel<false, false, 32, 4><<<grid, kThreads, 0, s>>>(
+          Xh, n_rows, ldx, C, nullptr, items, H, partials, accumulate, zero_row);
     }
     if (int rc = check_launch("hessian syrk")) return rc;
   }
   if (h.n_split > 0) {
-    dim3 grid(64, static_cast<unsigned>(h.n_split));
+    dim3 grid((kTile / kRedSub) * (kTile / kRedSub), static_cast<unsigned>(h.n_split));
     reduce_split_kernel<<<grid, 256, 0, s>>>(split, partials, H, C, accumulate);
     if (int rc = check_launch("hessian split reduce")) return rc;
   }

@@ -64,6 +64,30 @@ def test_grouped_gathered_hessian():
         assert torch.equal(H[gi], H[gi].T)
 
 
+def test_gathered_hessian_wide_addressing(monkeypatch):
+    """The 64-bit per-token row addressing used when X spans more than 4 GB,
+    forced on a small X: same H as the 32-bit row-offset form, bit for bit."""
+    from mlx_gptq import capture
+
+    C, N = 512, 3000
+    X = _rows(N, C, seed=8).to(DEV)
+    g = torch.Generator().manual_seed(9)
+    sizes = [900, 0, 1300, 77]
+    idx = torch.cat([torch.randint(0, N, (s,), generator=g) for s in sizes]).to(torch.int32)
+    off = [0]
+    for s in sizes:
+        off.append(off[-1] + s)
+    H32 = capture.grouped_hessian(X, off, row_index=idx.to(DEV))
+    monkeypatch.setenv("MGQ_HESSIAN_WIDE_ADDR", "1")
+    H64 = capture.grouped_hessian(X, off, row_index=idx.to(DEV))
+    assert torch.equal(H32, H64)
+    Xc = X.cpu()
+    for gi, s in enumerate(sizes):
+        if s:
+            rows = Xc[idx[off[gi] : off[gi + 1]].long()]
+            assert hessian_ref.rel_frobenius(H64[gi].cpu(), hessian_ref.hessian_fp64(rows)) < TOL
+
+
 def test_split_k_partials_and_accumulate():
     from mlx_gptq import capture
 
