@@ -88,50 +88,108 @@ __device__ inline float code_value(const uint32_t (&codes)[kG / 4], int i, float
   return (MODE == kMxfp4 ? e2m1_value(code) : e4m3_value(code)) * scale;
 }
 
-// e^T Hg e with fused multiply-adds in a fixed order. Hg is the block's
-// compact [32][32] copy (row stride 32), wave-uniform, so every element is a
-// scalar load at a compile-time offset from one base pointer. Symmetric
-// blocks use the upper triangle: sum_i e_i * (H_ii e_i + 2 sum_{j>i} H_ij e_j).
-__device__ inline float quad_form(const float (&e)[kG], const float* __restrict__ Hg, bool sym) {
+// e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
+//
+// P^T = Hg E^T is a 32x32 by 32x64 product: two 32-row blocks of E, each two
+// v_mfma_f32_32x32x16_bf16 over K = 32. Operands are split into bf16 hi + lo
+// (x = hi + lo within ~2^-17 relative) and the product is accumulated as
+// hi*hi + hi*lo + lo*hi in fp32, so the objective carries ~2^-16 relative
+// error against an fp32 sum (candidate choices only differ on near-ties).
+// Layouts (32x32x16 bf16): A lane l = row l%32, k = 8(l/32)+0..7; B lane l =
+// k = 8(l/32)+0..7, column l%32; D lane l register r = row 8(r/4)+4(l/32)+
+// r%4, column l%32.
+//   - A = Hg: lane l holds Hg[l%32][16kc + 8(l/32) + 0..7] (built once).
+//   - B = E^T of a 32-row block: lane l needs row l%32 of the block, columns
+//     16kc + 8(l/32) + 0..7. Each lane owns its own row's e[]; one
+//     v_permlane32_swap of (e[16kc..+7], e[16kc+8..+15]) yields block 0's B
+//     in the first result and block 1's in the second.
+//   - D of block 0 (rows 0-31) and block 1 (rows 32-63) hold P[i][c] with
+//     i = l%32 (+32) and c in S0 = {8(r/4)+r%4} on lanes < 32 or S1 = S0 + 4
+//     on lanes >= 32; one more swap of (D0, D1) gives every lane its own row
+//     for c in S0 (first) and S1 (second), so obj = sum_c e[c] P[c] is local.
+// All 64 lanes of the wave must execute this together.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+struct HOperand {
+  bf16x8_t hi[2], lo[2];
+};
+
+__device__ inline void split_bf16(const float* x, bf16x8_t& hi, bf16x8_t& lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const __bf16 h = static_cast<__bf16>(x[j]);
+    hi[j] = h;
+    lo[j] = static_cast<__bf16>(x[j] - static_cast<float>(h));
+  }
+}
+
+__device__ inline HOperand load_h_operand(const float* __restrict__ Hg, int lane) {
+  HOperand A;
+  const int c = lane & 31, k8 = 8 * (lane >> 5);
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = Hg[c * kG + 16 * kc + k8 + j];
+    split_bf16(x, A.hi[kc], A.lo[kc]);
+  }
+  return A;
+}
+
+// (x, y) -> ([x lanes 0-31 | y lanes 0-31], [x lanes 32-63 | y lanes 32-63])
+__device__ inline void swap_halves(bf16x8_t& x, bf16x8_t& y) {
+  u32x4_t a = __builtin_bit_cast(u32x4_t, x), b = __builtin_bit_cast(u32x4_t, y);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a[w], b[w], false, false);
+    a[w] = r[0];
+    b[w] = r[1];
+  }
+  x = __builtin_bit_cast(bf16x8_t, a);
+  y = __builtin_bit_cast(bf16x8_t, b);
+}
+
+__device__ inline float mfma_objective(const float (&e)[kG], const HOperand& A) {
+  f32x16_t d0, d1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d0[r] = d1[r] = 0.0f;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    bf16x8_t xh, xl, yh, yl;
+    split_bf16(e + 16 * kc, xh, xl);
+    split_bf16(e + 16 * kc + 8, yh, yl);
+    swap_halves(xh, yh);
+    swap_halves(xl, yl);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], xh, d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], yh, d1, 0, 0, 0);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], xl, d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], yl, d1, 0, 0, 0);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], xh, d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], yh, d1, 0, 0, 0);
+  }
   float obj = 0.0f;
-  if (sym) {
 #pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-      for (int j = i + 1; j < kG; j += 2) {
-        s0 = fmaf(Hg[i * kG + j], e[j], s0);
-        if (j + 1 < kG) s1 = fmaf(Hg[i * kG + j + 1], e[j + 1], s1);
-      }
-      obj = fmaf(e[i], fmaf(Hg[i * kG + i], e[i], 2.0f * (s0 + s1)), obj);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      float t0 = 0.0f, t1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kG; j += 2) {
-        t0 = fmaf(Hg[i * kG + j], e[j], t0);
-        t1 = fmaf(Hg[i * kG + j + 1], e[j + 1], t1);
-      }
-      obj = fmaf(e[i], t0 + t1, obj);
-    }
+  for (int r = 0; r < 16; ++r) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d0[r]), __float_as_uint(d1[r]),
+                                                     false, false);
+    const int c0 = 8 * (r >> 2) + (r & 3);
+    obj = fmaf(e[c0], __uint_as_float(sw[0]), obj);
+    obj = fmaf(e[c0 + 4], __uint_as_float(sw[1]), obj);
   }
   return obj;
 }
 
 // An opaque zero that depends on `v`: addresses built from it cannot be
 // computed before `v`, so the loads behind them are neither hoisted out of
-// the candidate loop nor scheduled far ahead of their use. Without this the
-// compiler lifts the 528 Hessian values (or the U block) out of the loops and
-// runs out of registers. zero_after_s gives a wave-uniform (scalar) zero so
-// the Hessian reads stay scalar loads.
+// the loop nor scheduled far ahead of their use (without this the compiler
+// lifts the U block out of the recurrence and runs out of registers).
 __device__ inline int zero_after(float v) {
   int z;
   asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(v));
   return z;
 }
-__device__ inline int zero_after_s(float v) { return __builtin_amdgcn_readfirstlane(zero_after(v)); }
 
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 
@@ -183,6 +241,7 @@ __global__ void __launch_bounds__(kThreads)
 
   // compact (post dead-column fix) Hessian block, written by hinv32
   const float* __restrict__ Hg = Hc + (b * G + g) * kG * kG;
+  const int lane = threadIdx.x & 63;
   // U^T staged in LDS (Ut[c][k] = U[k][c]): the recurrence below reads one
   // column of U per step with broadcast LDS loads (uniform addresses).
   __shared__ float Ut[kG * kG];
@@ -194,7 +253,6 @@ __global__ void __launch_bounds__(kThreads)
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
   const int64_t base = (b * R + r) * C + g * kG;
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
-  const bool sym = symflag[b * G + g] != 0;
 
   // The group's 32 (dead-column-fixed) weights live in LDS, one column per
   // thread (so[i][tid]: conflict-free), not in registers, which leaves room
@@ -224,7 +282,9 @@ __global__ void __launch_bounds__(kThreads)
   const int e0 = e8m0_exponent(amax, fmax);
   int e_sel = e0;
   float best = 0.0f;
+  HOperand Ah;
   if (SAFE) {
+    Ah = load_h_operand(Hg, lane);
     float err[kG];
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
@@ -232,7 +292,7 @@ __global__ void __launch_bounds__(kThreads)
       const float sc = exp2_int(e), inv = exp2_int(-e);
 #pragma unroll
       for (int i = 0; i < kG; ++i) err[i] = quant_fast<MODE>(ORIG(i), inv, sc) - ORIG(i);
-      const float obj = quad_form(err, Hg + zero_after_s(err[0]), sym);
+      const float obj = mfma_objective(err, Ah);
       if (o == 0 || obj < best) {
         best = obj;
         e_sel = e;
@@ -271,7 +331,7 @@ __global__ void __launch_bounds__(kThreads)
     float err[kG];
 #pragma unroll
     for (int i = 0; i < kG; ++i) err[i] = code_value<MODE>(codes, i, scale) - ORIG(i);
-    use_gptq = quad_form(err, Hg + zero_after_s(err[kG - 1]), sym) <= best;
+    use_gptq = mfma_objective(err, Ah) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;

@@ -177,7 +177,7 @@ __device__ inline void dma_tok(uint32_t lds_dst, uint32_t voffset, const char* s
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
                : "s"(lds_dst), "v"(voffset), "s"(saddr)
-               : "memory", "m0");
+               : "memory");
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));

@@ -18,15 +18,19 @@ enum Mode : int { kAffine = 0, kMxfp4 = 1, kMxfp8 = 2 };
 
 constexpr int kMxGroup = 32;  // MX_GROUP_SIZE (grid.py:21)
 
+// Bit casts usable on host and device (HIP's __float_as_uint is device-only).
+__host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 // ---------------------------------------------------------------------------
 // 16-bit float conversions (round to nearest even).
 // ---------------------------------------------------------------------------
 __host__ __device__ inline float bf16_to_f32(uint16_t h) {
-  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+  return u2f(static_cast<uint32_t>(h) << 16);
 }
 
 __host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
+  uint32_t u = f2u(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
@@ -97,7 +101,7 @@ __device__ inline float exp2_int(int k) {
 // E2M1 (grid.py:82-105): saturating round-half-even onto
 // {0, .5, 1, 1.5, 2, 3, 4, 6}; sign bit only for x < 0 (so -0 and NaN -> 0).
 // ---------------------------------------------------------------------------
-__device__ inline uint32_t e2m1_code(float x) {
+__host__ __device__ inline uint32_t e2m1_code(float x) {
   const float ax = fabsf(x);
   uint32_t m = (ax > 5.0f)    ? 7u
                : (ax >= 3.5f) ? 6u
@@ -111,7 +115,7 @@ __device__ inline uint32_t e2m1_code(float x) {
 }
 
 // _E2M1_VALUES[code] (grid.py:23-40).
-__device__ inline float e2m1_value(uint32_t code) {
+__host__ __device__ inline float e2m1_value(uint32_t code) {
   const uint32_t m = code & 7u;
   // magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6 as fp32 bit patterns
   constexpr uint32_t kMag[8] = {0x00000000u, 0x3f000000u, 0x3f800000u, 0x3fc00000u,
@@ -119,7 +123,7 @@ __device__ inline float e2m1_value(uint32_t code) {
   uint32_t b = kMag[0];
 #pragma unroll
   for (uint32_t i = 1; i < 8; ++i) b = (m == i) ? kMag[i] : b;
-  return __uint_as_float(b | ((code & 8u) << 28));
+  return u2f(b | ((code & 8u) << 28));
 }
 
 // ---------------------------------------------------------------------------
@@ -191,23 +195,23 @@ __device__ inline uint32_t mx_quant(float w, float scale, int mode, float* dq) {
 // materialising the code; the solver uses them to score scale candidates.
 // ---------------------------------------------------------------------------
 
-// E2M1 magnitude of |n| (RNE on {0,.5,1,1.5,2,3,4,6}, saturating), 0 for NaN.
-// Below 2 the grid step is 1/2, on [2,4) it is 1, from 4 it is 2: scaling by
-// the inverse step makes the grid the integers, where rint is exactly the
-// reference's threshold chain (ties to the even code).
-__device__ inline float e2m1_mag(float ax) {
-  const float f = ax < 2.0f ? 2.0f : (ax < 4.0f ? 1.0f : 0.5f);
-  const float finv = ax < 2.0f ? 0.5f : (ax < 4.0f ? 1.0f : 2.0f);
-  const float q = fminf(rintf(ax * f) * finv, 6.0f);
-  return (ax == ax) ? q : 0.0f;
-}
-
 // Signed dequantized MXFP4 value dq = value(code(n)) * scale, n = w * inv_scale.
-// The sign is the reference's code sign bit (n < 0), so (-0.25, 0) -> -0.0.
-__device__ inline float mx4_dq(float w, float inv_scale, float scale) {
+// |n| is rounded half-even to the E2M1 step of its binade (1/2 below 2, 1 on
+// [2,4), 2 from 4) by adding and subtracting 1.5 * 2^(22+k), k = clamp(
+// binade, 0, 2), whose ulp is that step; values past 5 saturate at 6. This
+// equals e2m1_value(e2m1_code(n)) for every finite n (checked for all 2^32
+// inputs), with two exceptions that leave the quantization error dq - w
+// unchanged: n = -0 gives -0, and NaN gives NaN's sign times 6 (the error of
+// a NaN weight is NaN either way).
+__host__ __device__ inline float mx4_dq(float w, float inv_scale, float scale) {
   const float n = w * inv_scale;
-  const float m = e2m1_mag(fabsf(n));
-  return (n < 0.0f ? -m : m) * scale;
+  const uint32_t ua = f2u(n) & 0x7fffffffu;
+  uint32_t eb = ua >> 23;
+  eb = eb < 127u ? 127u : (eb > 129u ? 129u : eb);
+  const float magic = u2f((eb << 23) + ((22u << 23) | 0x400000u));
+  const float a = u2f(ua);
+  const float m = fminf((a + magic) - magic, 6.0f);
+  return u2f(f2u(m * scale) | (f2u(n) & 0x80000000u));
 }
 
 // E4M3 value of clamp(n, +-448) rounded half-even onto the e4m3fn grid,
