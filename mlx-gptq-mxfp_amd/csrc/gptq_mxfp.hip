@@ -23,6 +23,8 @@
 // Objectives are fp32 sums in a fixed order (not torch's einsum order), so
 // near-exact ties between candidates may resolve differently from the
 // reference; every encoding itself is bit-exact.
+#include <type_traits>
+
 #include "mgq_capi.h"
 #include "mgq_common.h"
 
@@ -65,8 +67,7 @@ __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, fl
   uint32_t code;
   float v;
   if (MODE == kMxfp4) {
-    code = e2m1_code(n);
-    v = e2m1_value(code);
+    return mx4_encode(w, inv_scale, scale, dq);
   } else {
     code = e4m3_code_clamped(clamp448(n));
     v = e4m3_value(code);
@@ -78,14 +79,6 @@ __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, fl
 template <int MODE>
 __device__ inline float quant_fast(float w, float inv_scale, float scale) {
   return MODE == kMxfp4 ? mx4_dq(w, inv_scale, scale) : mx8_dq(w, inv_scale, scale);
-}
-
-// value(code) * scale for code i of a packed group: exactly the dq that
-// quant_exact returned for that code.
-template <int MODE>
-__device__ inline float code_value(const uint32_t (&codes)[kG / 4], int i, float scale) {
-  const uint32_t code = (codes[i / 4] >> (8 * (i % 4))) & 0xffu;
-  return (MODE == kMxfp4 ? e2m1_value(code) : e4m3_value(code)) * scale;
 }
 
 // e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
@@ -256,8 +249,10 @@ __global__ void __launch_bounds__(kThreads)
 
   // The group's 32 (dead-column-fixed) weights live in LDS, one column per
   // thread (so[i][tid]: conflict-free), not in registers, which leaves room
-  // for 3 waves per SIMD without spills.
-  __shared__ float so[kG * kThreads];
+  // for 3 waves per SIMD without spills. 16-bit inputs are kept as their own
+  // bits (exact), which halves the array.
+  using OrigT = std::conditional_t<sizeof(TIn) == 2, uint16_t, float>;
+  __shared__ OrigT so[kG * kThreads];
   float amax;
   {
     float v[kG];
@@ -273,25 +268,80 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(v[i]));
 #pragma unroll
-    for (int i = 0; i < kG; ++i) so[i * kThreads + threadIdx.x] = v[i];
+    for (int i = 0; i < kG; ++i) {
+      if constexpr (sizeof(TIn) == 4)
+        so[i * kThreads + threadIdx.x] = v[i];
+      else if constexpr (IS_F16)
+        so[i * kThreads + threadIdx.x] = f32_to_f16_rne(v[i]);
+      else
+        so[i * kThreads + threadIdx.x] = static_cast<uint16_t>(f2u(v[i]) >> 16);
+    }
   }
-  const float* orig = so + threadIdx.x;  // orig[i * kThreads] = weight i
-#define ORIG(i) orig[(i) * kThreads]
+  const OrigT* orig = so + threadIdx.x;  // orig[i * kThreads] = weight i
+  auto orig_at = [](const OrigT* p, int i) __attribute__((always_inline)) -> float {
+    if constexpr (sizeof(TIn) == 4)
+      return p[i * kThreads];
+    else if constexpr (IS_F16)
+      return f16_to_f32(p[i * kThreads]);
+    else
+      return bf16_to_f32(p[i * kThreads]);
+  };
+#define ORIG(i) orig_at(orig, (i))
+  // The dequantized values of the selected result: in LDS (same layout)
+  // for the safe search, whose candidate objectives need the registers; in
+  // registers for the groupwise solve, which keeps that kernel's LDS small.
+  // MXFP4 values (at most 2 significant bits times a power of two >= 2^-128)
+  // are exact in bf16, so they are stored as the top half of their fp32 bits.
+  using DqT = std::conditional_t<MODE == kMxfp4, uint16_t, float>;
+  float dqr[SAFE ? 1 : kG];
+  DqT* dqs = nullptr;
+  if constexpr (SAFE) {
+    __shared__ DqT sdq[kG * kThreads];
+    dqs = sdq + threadIdx.x;
+  }
+  auto dq_get = [&](int i) __attribute__((always_inline)) -> float {
+    if constexpr (!SAFE)
+      return dqr[i];
+    else if constexpr (MODE == kMxfp4)
+      return bf16_to_f32(dqs[i * kThreads]);
+    else
+      return dqs[i * kThreads];
+  };
+  auto dq_set = [&](int i, float v) __attribute__((always_inline)) {
+    if constexpr (!SAFE)
+      dqr[i] = v;
+    else if constexpr (MODE == kMxfp4)
+      dqs[i * kThreads] = static_cast<uint16_t>(f2u(v) >> 16);
+    else
+      dqs[i * kThreads] = v;
+  };
+#define DQ(i) dq_get(i)
 
   // 1. scale choice
   const int e0 = e8m0_exponent(amax, fmax);
   int e_sel = e0;
   float best = 0.0f;
-  HOperand Ah;
   if (SAFE) {
-    Ah = load_h_operand(Hg, lane);
+    const HOperand Ah = load_h_operand(Hg, lane);
     float err[kG];
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
       const float sc = exp2_int(e), inv = exp2_int(-e);
+      // re-read the weights from LDS per candidate (an opaque offset keeps
+      // the compiler from holding all 32 in registers across the loop)
+      const OrigT* og = orig + zero_after(sc);
+      // eight elements at a time: the scheduler would otherwise run each op
+      // over all 32 elements before the next and hold 4 x 32 temporaries
 #pragma unroll
-      for (int i = 0; i < kG; ++i) err[i] = quant_fast<MODE>(ORIG(i), inv, sc) - ORIG(i);
+      for (int i0 = 0; i0 < kG; i0 += 8) {
+#pragma unroll
+        for (int i = i0; i < i0 + 8; ++i) {
+          const float x = orig_at(og, i);
+          err[i] = quant_fast<MODE>(x, inv, sc) - x;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
       const float obj = mfma_objective(err, Ah);
       if (o == 0 || obj < best) {
         best = obj;
@@ -307,8 +357,7 @@ __global__ void __launch_bounds__(kThreads)
   // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
   // Forming w_c lazily from the stored errors performs exactly those
   // roundings while keeping only err[] live.
-  // The dequantized values are not kept: they are value(code) * scale,
-  // decoded again below, which keeps 32 registers free.
+  // The dequantized values go to LDS (DQ), which keeps 32 registers free.
   float errs[kG];
   uint32_t codes[kG / 4];
 #pragma unroll
@@ -323,6 +372,7 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
     errs[c] = (acc - dq) / col[c];
     codes[c / 4] |= code << (8 * (c % 4));
+    dq_set(c, dq);
   }
 
   // 3. GPTQ vs best RTN candidate (safe search only)
@@ -330,8 +380,15 @@ __global__ void __launch_bounds__(kThreads)
   if (SAFE) {
     float err[kG];
 #pragma unroll
-    for (int i = 0; i < kG; ++i) err[i] = code_value<MODE>(codes, i, scale) - ORIG(i);
-    use_gptq = mfma_objective(err, Ah) <= best;
+    for (int i0 = 0; i0 < kG; i0 += 8) {
+#pragma unroll
+      for (int i = i0; i < i0 + 8; ++i) err[i] = DQ(i) - ORIG(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the H operand again (an opaque offset: a fresh load, not registers held
+    // through the recurrence)
+    const HOperand Ah2 = load_h_operand(Hg + zero_after(err[0]), lane);
+    use_gptq = mfma_objective(err, Ah2) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;
@@ -340,7 +397,7 @@ __global__ void __launch_bounds__(kThreads)
   bool ok = use_gptq;
   if (use_gptq) {
 #pragma unroll
-    for (int i = 0; i < kG; ++i) ok = ok && (fabsf(code_value<MODE>(codes, i, scale)) <= limit);
+    for (int i = 0; i < kG; ++i) ok = ok & (fabsf(DQ(i)) <= limit);  // no short-circuit branches
   }
   if (!ok) {  // RTN baseline at the chosen scale
 #pragma unroll
@@ -350,11 +407,12 @@ __global__ void __launch_bounds__(kThreads)
       float dq;
       const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
       codes[i / 4] |= code << (8 * (i % 4));
+      dq_set(i, dq);
     }
   }
   float w[kG];
 #pragma unroll
-  for (int i = 0; i < kG; ++i) w[i] = code_value<MODE>(codes, i, scale);
+  for (int i = 0; i < kG; ++i) w[i] = DQ(i);
 
   double num = 0.0, den = 0.0;
   if (valid) {
@@ -403,6 +461,7 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 #undef ORIG
+#undef DQ
 
 // rel[b] = sqrt(sum num) / max(sqrt(sum den), 1e-12), partials summed in order.
 __global__ void rel_err_kernel(const double* __restrict__ part, int64_t n_per_b, int64_t B,

@@ -214,6 +214,27 @@ __host__ __device__ inline float mx4_dq(float w, float inv_scale, float scale) {
   return u2f(f2u(m * scale) | (f2u(n) & 0x80000000u));
 }
 
+// Exact MXFP4 encoding of n = w * inv_scale without a compare chain: the
+// magnitude comes from the same half-even rounding as mx4_dq, and the code
+// from its bit pattern (f2u(m) >> 22 is 0 for 0, 252 for 0.5 and 254..259 for
+// 1, 1.5, 2, 3, 4, 6). Code and dq equal e2m1_code(n) and
+// e2m1_value(code) * scale for every fp32 n, NaN and -0 included (checked
+// for all 2^32 inputs).
+__host__ __device__ inline uint32_t mx4_encode(float w, float inv_scale, float scale, float* dq) {
+  const float n = w * inv_scale;
+  const uint32_t ua = f2u(n) & 0x7fffffffu;
+  uint32_t eb = ua >> 23;
+  eb = eb < 127u ? 127u : (eb > 129u ? 129u : eb);
+  const float magic = u2f((eb << 23) + ((22u << 23) | 0x400000u));
+  float m = fminf((u2f(ua) + magic) - magic, 6.0f);
+  m = (n == n) ? m : 0.0f;
+  const uint32_t t = f2u(m) >> 22;
+  const uint32_t mag = t >= 254u ? t - 252u : (t != 0u ? 1u : 0u);
+  const bool neg = n < 0.0f;
+  *dq = (neg ? -m : m) * scale;
+  return mag | (neg ? 8u : 0u);
+}
+
 // E4M3 value of clamp(n, +-448) rounded half-even onto the e4m3fn grid,
 // sign preserved, NaN stays NaN.
 __device__ inline float e4m3_round(float n) {

@@ -1,10 +1,13 @@
-// Exhaustive host check of the solver's MXFP4 fast projection (mgq::mx4_dq,
-// used to score safe-scale-search candidates) against the exact encoder
-// e2m1_value(e2m1_code(n)) (the grid.py:82-105 threshold chain), for all 2^32
-// fp32 inputs n (inv_scale = scale = 1; scales are powers of two, so every
-// other scale is the same check on n = w * 2^-e). Allowed differences: NaN
-// inputs and the sign of a zero result, which leave the error dq - w
-// unchanged. Prints the number of other mismatches; exit status 0 iff none.
+// Exhaustive host check of the solver's MXFP4 encoders against the exact
+// threshold chain e2m1_code / e2m1_value (grid.py:82-105), for all 2^32 fp32
+// inputs n (inv_scale = scale = 1; scales are powers of two, so every other
+// scale is the same check on n = w * 2^-e):
+//   - mgq::mx4_encode (code and dq, used by the GPTQ recurrence) must agree
+//     bit for bit;
+//   - mgq::mx4_dq (used to score safe-scale-search candidates) may differ
+//     only on NaN inputs and in the sign of a zero result, which leave the
+//     error dq - w unchanged.
+// Prints the number of other mismatches; exit status 0 iff there are none.
 #include <cstdio>
 #include <thread>
 #include <vector>
@@ -20,8 +23,15 @@ int main() {
       const uint64_t lo = (uint64_t(1) << 32) / T * t, hi = (uint64_t(1) << 32) / T * (t + 1);
       for (uint64_t i = lo; i < hi; ++i) {
         const float n = mgq::u2f(static_cast<uint32_t>(i));
+        const uint32_t code = mgq::e2m1_code(n);
+        const float exact = mgq::e2m1_value(code);
+        float enc_dq;
+        const uint32_t enc_code = mgq::mx4_encode(n, 1.0f, 1.0f, &enc_dq);
+        if (enc_code != code || mgq::f2u(enc_dq) != mgq::f2u(exact)) {
+          if (++bad[t] <= 4) printf("encode mismatch n=%a code=%u/%u dq=%a/%a\n", n, enc_code, code, enc_dq, exact);
+          continue;
+        }
         const float fast = mgq::mx4_dq(n, 1.0f, 1.0f);
-        const float exact = mgq::e2m1_value(mgq::e2m1_code(n));
         if (mgq::f2u(fast) == mgq::f2u(exact)) continue;
         if (n != n) continue;
         if (fast == 0.0f && exact == 0.0f) continue;

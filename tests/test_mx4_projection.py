@@ -1,6 +1,6 @@
 """Exhaustive CPU check of the MXFP4 fast projection the solver uses to score
 safe-scale-search candidates (csrc/mgq_common.h mx4_dq) against the exact
-E2M1 encoder (e2m1_code / e2m1_value, the grid.py:82-105 threshold chain),
+E2M1 encoder (e2m1_code / e2m1_value, the grid.py:82-105 threshold chain), and of the compare-free exact encoder mx4_encode,
 over all 2^32 fp32 inputs. Compiles the header for the host with hipcc."""
 
 from __future__ import annotations
