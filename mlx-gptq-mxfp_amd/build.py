@@ -39,6 +39,13 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source extra flags. The MXFP solver's candidate objective keeps its
+# small MFMA accumulators in ordinary VGPRs (they feed VALU code right away);
+# the Hessian kernel keeps the default, which puts its 256 accumulators in
+# AGPRs.
+EXTRA_FLAGS = {"gptq_mxfp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -48,7 +55,8 @@ def hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-I", str(CSRC), "-c", str(src),
+           "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -184,6 +184,19 @@ __device__ inline int zero_after(float v) {
   return z;
 }
 
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) f32x4_t lds_f32x4;
+
+// The LDS address p, opaque to the compiler and ordered after `dep`: reads at
+// small offsets from it use one base register (their immediate offsets fit),
+// and they are not hoisted above the value they wait for.
+__device__ inline const lds_f32* lds_after(const lds_f32* p, float dep) {
+  uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+  asm volatile("; lds_after %1" : "+v"(a) : "v"(dep));
+  return reinterpret_cast<const lds_f32*>(static_cast<uintptr_t>(a));
+}
+
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 
 // The 32 weights of one (row, group), 16-byte loads, widened to fp32.
@@ -364,10 +377,16 @@ __global__ void __launch_bounds__(kThreads)
   for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
   for (int c = 0; c < kG; ++c) {
-    const float* col = Ut + c * kG + (c ? zero_after(errs[c - 1]) : 0);
+    // column c of U (row c of Ut, 16-byte aligned), read 4 values at a time
+    const lds_f32* col = (const lds_f32*)Ut + c * kG;
+    if (c) col = lds_after(col, errs[c - 1]);
     float acc = ORIG(c);
 #pragma unroll
-    for (int k = 0; k < c; ++k) acc = acc - errs[k] * col[k];
+    for (int k0 = 0; k0 < c; k0 += 4) {
+      const f32x4_t u4 = *reinterpret_cast<const lds_f32x4*>(col + k0);
+#pragma unroll
+      for (int k = k0; k < c && k < k0 + 4; ++k) acc = acc - errs[k] * u4[k - k0];
+    }
     float dq;
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
     errs[c] = (acc - dq) / col[c];
