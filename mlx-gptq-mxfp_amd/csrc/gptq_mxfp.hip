@@ -76,9 +76,16 @@ __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, fl
   return code;
 }
 
+// (dq - w) / scale for scoring a scale candidate (quant_exact's dq minus w,
+// in units of the scale, without materialising the code).
 template <int MODE>
-__device__ inline float quant_fast(float w, float inv_scale, float scale) {
-  return MODE == kMxfp4 ? mx4_dq(w, inv_scale, scale) : mx8_dq(w, inv_scale, scale);
+__device__ inline float quant_err(float w, float inv_scale) {
+  if constexpr (MODE == kMxfp4) {
+    return mx4_err(w, inv_scale);
+  } else {
+    const float n = w * inv_scale;
+    return e4m3_round(n) - n;
+  }
 }
 
 // e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
@@ -333,6 +340,9 @@ __global__ void __launch_bounds__(kThreads)
   // 1. scale choice
   const int e0 = e8m0_exponent(amax, fmax);
   int e_sel = e0;
+  // Objectives are computed on errors in units of the candidate's scale and
+  // multiplied by 2^(2 (e - e0)), which is exact: the comparisons are those
+  // of the scaled objectives, without scaling every error.
   float best = 0.0f;
   if (SAFE) {
     const HOperand Ah = load_h_operand(Hg, lane);
@@ -340,10 +350,10 @@ __global__ void __launch_bounds__(kThreads)
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
-      const float sc = exp2_int(e), inv = exp2_int(-e);
+      const float inv = exp2_int(-e);
       // re-read the weights from LDS per candidate (an opaque offset keeps
       // the compiler from holding all 32 in registers across the loop)
-      const OrigT* og = orig + zero_after(sc);
+      const OrigT* og = orig + zero_after(inv);
       // eight elements at a time: the scheduler would otherwise run each op
       // over all 32 elements before the next and hold 4 x 32 temporaries
 #pragma unroll
@@ -351,11 +361,11 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int i = i0; i < i0 + 8; ++i) {
           const float x = orig_at(og, i);
-          err[i] = quant_fast<MODE>(x, inv, sc) - x;
+          err[i] = quant_err<MODE>(x, inv);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      const float obj = mfma_objective(err, Ah);
+      const float obj = mfma_objective(err, Ah) * exp2_int(2 * (e - e0));
       if (o == 0 || obj < best) {
         best = obj;
         e_sel = e;
@@ -401,13 +411,13 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int i0 = 0; i0 < kG; i0 += 8) {
 #pragma unroll
-      for (int i = i0; i < i0 + 8; ++i) err[i] = DQ(i) - ORIG(i);
+      for (int i = i0; i < i0 + 8; ++i) err[i] = (DQ(i) - ORIG(i)) * inv_scale;
       __builtin_amdgcn_sched_barrier(0);
     }
     // the H operand again (an opaque offset: a fresh load, not registers held
     // through the recurrence)
     const HOperand Ah2 = load_h_operand(Hg + zero_after(err[0]), lane);
-    use_gptq = mfma_objective(err, Ah2) <= best;
+    use_gptq = mfma_objective(err, Ah2) * exp2_int(2 * (e_sel - e0)) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;

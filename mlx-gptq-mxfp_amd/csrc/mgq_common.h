@@ -195,27 +195,29 @@ __device__ inline uint32_t mx_quant(float w, float scale, int mode, float* dq) {
 // materialising the code; the solver uses them to score scale candidates.
 // ---------------------------------------------------------------------------
 
-// Signed dequantized MXFP4 value dq = value(code(n)) * scale, n = w * inv_scale.
-// |n| is rounded half-even to the E2M1 step of its binade (1/2 below 2, 1 on
-// [2,4), 2 from 4) by adding and subtracting 1.5 * 2^(22+k), k = clamp(
-// binade, 0, 2), whose ulp is that step; values past 5 saturate at 6. This
-// equals e2m1_value(e2m1_code(n)) for every finite n (checked for all 2^32
-// inputs), with two exceptions that leave the quantization error dq - w
-// unchanged: n = -0 gives -0, and NaN gives NaN's sign times 6 (the error of
-// a NaN weight is NaN either way).
-__host__ __device__ inline float mx4_dq(float w, float inv_scale, float scale) {
+// Quantization error of MXFP4 in units of the scale: (dq - w) / scale with
+// dq = value(code(n)) * scale, n = w * inv_scale, for scoring scale
+// candidates. n is rounded half-even to the E2M1 step of its binade (1/2
+// below 2, 1 on [2,4), 2 from 4) by adding and subtracting
+// 1.5 * 2^(22+k), k = clamp(binade, 0, 2), whose ulp is that step (symmetric
+// in the sign of n), then clamped to +-6. q - n is exact when q is the
+// rounding of n (it is n's discarded low bits) and is the reference's single
+// fp32 rounding when q saturates, so (q - n) * scale is the reference's
+// dq - w whenever that product stays normal. Equal to
+// e2m1_value(e2m1_code(n)) - n for every fp32 n (checked for all 2^32
+// inputs; NaN in, NaN out).
+__host__ __device__ inline float mx4_err(float w, float inv_scale) {
   const float n = w * inv_scale;
-  const uint32_t ua = f2u(n) & 0x7fffffffu;
-  uint32_t eb = ua >> 23;
+  uint32_t eb = (f2u(n) >> 23) & 0xffu;
   eb = eb < 127u ? 127u : (eb > 129u ? 129u : eb);
   const float magic = u2f((eb << 23) + ((22u << 23) | 0x400000u));
-  const float a = u2f(ua);
-  const float m = fminf((a + magic) - magic, 6.0f);
-  return u2f(f2u(m * scale) | (f2u(n) & 0x80000000u));
+  float q = (n + magic) - magic;
+  q = fminf(fmaxf(q, -6.0f), 6.0f);
+  return q - n;
 }
 
 // Exact MXFP4 encoding of n = w * inv_scale without a compare chain: the
-// magnitude comes from the same half-even rounding as mx4_dq, and the code
+// magnitude comes from the same half-even rounding as mx4_err, and the code
 // from its bit pattern (f2u(m) >> 22 is 0 for 0, 252 for 0.5 and 254..259 for
 // 1, 1.5, 2, 3, 4, 6). Code and dq equal e2m1_code(n) and
 // e2m1_value(code) * scale for every fp32 n, NaN and -0 included (checked

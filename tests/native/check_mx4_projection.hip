@@ -4,9 +4,9 @@
 // scale is the same check on n = w * 2^-e):
 //   - mgq::mx4_encode (code and dq, used by the GPTQ recurrence) must agree
 //     bit for bit;
-//   - mgq::mx4_dq (used to score safe-scale-search candidates) may differ
-//     only on NaN inputs and in the sign of a zero result, which leave the
-//     error dq - w unchanged.
+//   - mgq::mx4_err ((dq - w) / scale, used to score safe-scale-search
+//     candidates) must equal the fp32 difference e2m1_value(e2m1_code(n)) - n
+//     bit for bit (both NaN for NaN inputs).
 // Prints the number of other mismatches; exit status 0 iff there are none.
 #include <cstdio>
 #include <thread>
@@ -31,11 +31,11 @@ int main() {
           if (++bad[t] <= 4) printf("encode mismatch n=%a code=%u/%u dq=%a/%a\n", n, enc_code, code, enc_dq, exact);
           continue;
         }
-        const float fast = mgq::mx4_dq(n, 1.0f, 1.0f);
-        if (mgq::f2u(fast) == mgq::f2u(exact)) continue;
-        if (n != n) continue;
-        if (fast == 0.0f && exact == 0.0f) continue;
-        if (++bad[t] <= 4) printf("mismatch n=%a fast=%a exact=%a\n", n, fast, exact);
+        const float err = mgq::mx4_err(n, 1.0f);
+        const float ref = exact - n;  // the reference's fp32 error
+        if (mgq::f2u(err) == mgq::f2u(ref)) continue;
+        if (err != err && ref != ref) continue;
+        if (++bad[t] <= 4) printf("error mismatch n=%a err=%a ref=%a\n", n, err, ref);
       }
     });
   }

@@ -1,7 +1,9 @@
-"""Exhaustive CPU check of the MXFP4 fast projection the solver uses to score
-safe-scale-search candidates (csrc/mgq_common.h mx4_dq) against the exact
-E2M1 encoder (e2m1_code / e2m1_value, the grid.py:82-105 threshold chain), and of the compare-free exact encoder mx4_encode,
-over all 2^32 fp32 inputs. Compiles the header for the host with hipcc."""
+"""Exhaustive CPU check of the solver's MXFP4 arithmetic over all 2^32 fp32
+inputs, against the threshold-chain encoder e2m1_code / e2m1_value (the
+grid.py:82-105 restatement in csrc/mgq_common.h): the compare-free exact
+encoder mx4_encode (code and dq) and the quantization error mx4_err used to
+score safe-scale-search candidates. Compiles the header for the host with
+hipcc."""
 
 from __future__ import annotations
 
