@@ -77,6 +77,29 @@ __global__ void dead_fix_h_kernel(float* __restrict__ H, int64_t B, int64_t C) {
   }
 }
 
+// Four shrink candidates' error sums reduced together: the same butterfly
+// (and so the same rounding) as wave_sum, with the shuffle latencies of the
+// four chains overlapped.
+__device__ inline void wave_sum4(float (&v)[4]) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = __shfl_xor(v[i], off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] += t[i];
+  }
+}
+
+// Row k of U restricted to the group's columns: lane t holds U[k][j + t + 64 s].
+template <int CPL>
+__device__ inline void load_urow(const float* __restrict__ Ub, int64_t C, int64_t k, int64_t j,
+                                 int lane, const bool (&act)[CPL], float (&u)[CPL]) {
+  const float* Uk = Ub + k * C + j;
+#pragma unroll
+  for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
+}
+
 template <int CPL>
 __global__ void __launch_bounds__(kWaves * 64)
     affine_block_kernel(float* __restrict__ W, const float* __restrict__ U, int64_t B, int64_t R,
@@ -101,13 +124,30 @@ __global__ void __launch_bounds__(kWaves * 64)
       act[s] = col < G;
       acc[s] = act[s] ? Wr[j + col] : 0.0f;
     }
-    // earlier in-block updates, in column order
-    for (int64_t k = i1; k < j; ++k) {
-      const float e = errs[k - i1];
-      const float* Uk = Ub + k * C + j;
+    // earlier in-block updates, in column order; eight rows of U in flight
+    {
+      const int64_t kn = j - i1;  // a multiple of G
+      int64_t k = 0;
+      for (; k + 8 <= kn; k += 8) {
+        float u[8][CPL];
 #pragma unroll
-      for (int s = 0; s < CPL; ++s)
-        if (act[s]) acc[s] = acc[s] - e * Uk[lane + 64 * s];
+        for (int t = 0; t < 8; ++t) load_urow<CPL>(Ub, C, i1 + k + t, j, lane, act, u[t]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float e = errs[k + t];
+#pragma unroll
+          for (int s = 0; s < CPL; ++s)
+            if (act[s]) acc[s] = acc[s] - e * u[t][s];
+        }
+      }
+      for (; k < kn; ++k) {
+        float u[CPL];
+        load_urow<CPL>(Ub, C, i1 + k, j, lane, act, u);
+        const float e = errs[k];
+#pragma unroll
+        for (int s = 0; s < CPL; ++s)
+          if (act[s]) acc[s] = acc[s] - e * u[s];
+      }
     }
     // clip search (grid.py:167-212) on the group's current values
     float lo = act[0] ? acc[0] : __uint_as_float(0x7f800000u);
@@ -121,22 +161,31 @@ __global__ void __launch_bounds__(kWaves * 64)
     const float wmin = wave_nan_min(lo), wmax = wave_nan_max(hi);
     const float range = wmax - wmin;
     float best_err = 0.0f, s32 = 0.0f, b32 = 0.0f;
-    for (int cand = 0; cand < sh.n; ++cand) {
-      const float sc = round_to_storage(range * sh.p_over_maxq[cand], storage);
-      const float bi = round_to_storage(wmin * sh.p[cand], storage);
-      const float ss = (fabsf(sc) < 1e-12f) ? 1.0f : sc;
-      float part = 0.0f;
+    // candidates four at a time (the host pads the list to a multiple of 4
+    // with copies of the last one, which never win a strict '<')
+    for (int c0 = 0; c0 < sh.n; c0 += 4) {
+      float sc[4], bi[4], part[4];
 #pragma unroll
-      for (int s = 0; s < CPL; ++s)
-        if (act[s]) {
-          const float d = affine_q(acc[s], bi, ss, maxq) * sc + bi - acc[s];
-          part += d * d;
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = round_to_storage(range * sh.p_over_maxq[c0 + i], storage);
+        bi[i] = round_to_storage(wmin * sh.p[c0 + i], storage);
+        const float ss = (fabsf(sc[i]) < 1e-12f) ? 1.0f : sc[i];
+        part[i] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < CPL; ++s)
+          if (act[s]) {
+            const float d = affine_q(acc[s], bi[i], ss, maxq) * sc[i] + bi[i] - acc[s];
+            part[i] += d * d;
+          }
+      }
+      wave_sum4(part);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (c0 + i == 0 || part[i] < best_err) {
+          best_err = part[i];
+          s32 = sc[i];
+          b32 = bi[i];
         }
-      const float err = wave_sum(part);
-      if (cand == 0 || err < best_err) {
-        best_err = err;
-        s32 = sc;
-        b32 = bi;
       }
     }
     const int64_t gi = row * ng + j / G;
@@ -145,34 +194,59 @@ __global__ void __launch_bounds__(kWaves * 64)
       store_storage(b_store, gi, b32, storage);
     }
     const float s_safe = (fabsf(s32) < 1e-12f) ? 1.0f : s32;
-    // sequential columns of the group
-    for (int c = 0; c < G; ++c) {
+    // Sequential columns of the group. The column's value and U's diagonal
+    // are read from their owner lane (v_readlane, so every lane computes the
+    // same error); U rows arrive four columns ahead.
+    auto column = [&](int c, const float (&uc)[CPL]) __attribute__((always_inline)) {
       const int owner = c & 63, slot = c >> 6;
-      float mine = 0.0f;
+      float mine_v = acc[0], diag_v = uc[0];
 #pragma unroll
-      for (int s = 0; s < CPL; ++s)
-        if (s == slot) mine = acc[s];
+      for (int s = 1; s < CPL; ++s)
+        if (s == slot) {
+          mine_v = acc[s];
+          diag_v = uc[s];
+        }
+      const float mine = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine_v), owner));
+      const float diag = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, diag_v), owner));
       const float q = affine_q(mine, b32, s_safe, maxq);
       const float dq = q * s32 + b32;
-      const float diag = Ub[(j + c) * C + j + c];
-      const float e_lane = (mine - dq) / diag;
-      const float e = __shfl(e_lane, owner);
+      const float e = (mine - dq) / diag;
       if (lane == owner) {
         q_out[row * C + j + c] = (q == q) ? static_cast<uint8_t>(q) : 0;
         Wr[j + c] = dq;
         errs[j + c - i1] = e;
         Err[row * n + (j + c - i1)] = e;
       }
-      // errs[] is read by every lane of this wave at the next group start
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      const float* Uc = Ub + (j + c) * C + j;
 #pragma unroll
       for (int s = 0; s < CPL; ++s) {
         const int col = lane + 64 * s;
-        if (act[s] && col > c) acc[s] = acc[s] - e * Uc[col];
+        if (act[s] && col > c) acc[s] = acc[s] - e * uc[s];
+      }
+    };
+    const int G4 = G & ~3;
+    float ring[4][CPL];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (u < G4) load_urow<CPL>(Ub, C, j + u, j, lane, act, ring[u]);
+    for (int c0 = 0; c0 < G4; c0 += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u;
+        float uc[CPL];
+#pragma unroll
+        for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
+        if (c + 4 < G4) load_urow<CPL>(Ub, C, j + c + 4, j, lane, act, ring[u]);
+        column(c, uc);
       }
     }
+    for (int c = G4; c < G; ++c) {
+      float uc[CPL];
+      load_urow<CPL>(Ub, C, j + c, j, lane, act, uc);
+      column(c, uc);
+    }
+    // errs[] is read by every lane of this wave at the next group start
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -237,18 +311,27 @@ __global__ void __launch_bounds__(256)
 int make_shrinks(int bits, int method, int grid_steps, double max_shrink, Shrinks* out) {
   const double maxq = static_cast<double>((1 << bits) - 1);
   if (method == MGQ_CLIP_MINMAX) {
-    out->n = 1;
-    out->p_over_maxq[0] = static_cast<float>(1.0 / maxq);
-    out->p[0] = 1.0f;
+    out->n = 4;  // one candidate, padded to the kernel's batch of four
+    for (int i = 0; i < 4; ++i) {
+      out->p_over_maxq[i] = static_cast<float>(1.0 / maxq);
+      out->p[i] = 1.0f;
+    }
     return MGQ_OK;
   }
-  MGQ_REQUIRE(grid_steps >= 1 && grid_steps < kMaxShrinks, MGQ_ERR_VALUE,
-              "grid_steps must be in [1, %d)", kMaxShrinks);
+  MGQ_REQUIRE(grid_steps >= 1 && grid_steps < kMaxShrinks - 4, MGQ_ERR_VALUE,
+              "grid_steps must be in [1, %d)", kMaxShrinks - 4);
   out->n = grid_steps + 1;
   for (int i = 0; i <= grid_steps; ++i) {
     const double p = 1.0 - max_shrink * static_cast<double>(i) / static_cast<double>(grid_steps);
     out->p_over_maxq[i] = static_cast<float>(p / maxq);
     out->p[i] = static_cast<float>(p);
+  }
+  // the kernel scores candidates four at a time: pad with copies of the last
+  // one (an equal error never replaces the earlier best under strict '<')
+  while (out->n % 4) {
+    out->p_over_maxq[out->n] = out->p_over_maxq[out->n - 1];
+    out->p[out->n] = out->p[out->n - 1];
+    ++out->n;
   }
   return MGQ_OK;
 }
