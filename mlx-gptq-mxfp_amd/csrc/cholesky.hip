@@ -2,19 +2,35 @@
 //
 // For every square diagonal block Hb of size n (n = 32: the per-group blocks
 // of the MXFP solver, gptq.py:99-100) compute the upper-triangular U with
-//     U^T U = (Hb + lam I)^-1,   lam = damp * max(mean(diag Hb), 1e-8),
+//     U^T U = (Hd)^-1,   Hd = Hb + lam I,   lam = damp * max(mean(diag Hb), 1e-8),
 // escalating damp *= 10 (fp32, per block) until the factorisation succeeds,
 // at most max_attempts times, exactly as the reference escalates failed batch
-// items. Hd = Hb + lam I is formed in fp32 as the reference does; the
+// items. Hd is formed in fp32 as the reference does and, like
+// torch.linalg.cholesky_ex, only its lower triangle is read; the
 // factorisation and inverse run in fp64 and are rounded to fp32 once, so U
 // is the correctly rounded factor up to fp64 error.
 //
-// Method (one wavefront per block, fp64 in LDS): factor Hd = V V^T with V
-// upper triangular (Cholesky in reverse index order); then
-// (Hd)^-1 = V^-T V^-1 = W^T W with W = V^-1 upper, and by uniqueness of the
-// Cholesky factor U = W. This needs one factorisation and one triangular
-// inverse instead of the reference's factor / invert / re-factor sequence.
+// Method. Factor Hd = V V^T with V upper triangular (Cholesky in reverse
+// index order); then (Hd)^-1 = V^-T V^-1 = W^T W with W = V^-1 upper, and by
+// uniqueness of the Cholesky factor U = W. The reference's factor / invert /
+// re-factor sequence becomes one sweep over j = n-1 .. 0 that does the
+// factorisation step and the Gauss-Jordan step of the inverse together:
+// with a = row j of the working matrix (a_k = A[j][k] for k < j, the lower
+// triangle; a_j = d, the pivot; a_k = X[j][k] for k > j, the not yet scaled
+// row j of the inverse) and c_i = a_i / d, every row i < j does
+//     R[i][k] -= c_i a_k   (k != j),   R[i][j] = -c_i,
+// which is the trailing update A[i][k] -= V[i][j] V[k][j] for k < j and the
+// elimination X[i][k] -= V[i][j] X[j][k] / sqrt(d) for k >= j at once.
+// Row j is final after its step; at the end row i is scaled by 1/sqrt(d_i).
 // A pivot <= 0 or NaN fails the attempt (LAPACK potrf semantics).
+//
+// Layout: one wavefront per block, lanes as an 8 x 8 grid (p = lane / 8,
+// q = lane % 8), lane (p, q) holding rows 4p..4p+3 x columns 4q..4q+3 in 16
+// fp64 registers. Each step the 8 lanes that hold row j write it (256 bytes)
+// to the wave's LDS slot and every lane reads back the 4 entries of its rows
+// and the 4 of its columns. There is no workgroup barrier: the four waves
+// of a workgroup work on different blocks and LDS operations of one wave
+// complete in issue order.
 #include "mgq_capi.h"
 #include "mgq_common.h"
 
@@ -22,103 +38,138 @@ namespace mgq {
 namespace {
 
 constexpr int kN = 32;
+constexpr int kWaves = 4;  // blocks per workgroup, one wavefront each
+
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+
+// 1/d for d > 0: v_rcp_f64 refined by two Newton-Raphson steps
+// y <- y + y (1 - d y), each of which squares the relative error.
+__device__ inline double recip_f64(double d) {
+  double y = __builtin_amdgcn_rcp(d);
+  double e = fma(-d, y, 1.0);
+  y = fma(y, e, y);
+  e = fma(-d, y, 1.0);
+  return fma(y, e, y);
+}
+
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
 
 // attempts[g*B + b]: 1..max_attempts on success, 0 if every attempt failed.
-// sym[b*G + g] (optional): 1 when the undamped block is exactly symmetric.
 // Hc (optional): compact [B*G][32][32] copy of each undamped block.
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * kWaves)
     hinv32_kernel(const float* __restrict__ H, int64_t B, int64_t C, float damp,
                   int max_attempts, float* __restrict__ U, int32_t* __restrict__ attempts,
-                  uint8_t* __restrict__ sym, float* __restrict__ Hc) {
-  __shared__ double A[kN][kN + 1];
-  __shared__ double Wm[kN][kN + 1];
+                  float* __restrict__ Hc) {
+  __shared__ __attribute__((aligned(16))) double bcast[kWaves][kN];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int64_t G = C / kN;
-  const int64_t b = blockIdx.x / G;
-  const int64_t g = blockIdx.x % G;
-  const int lane = threadIdx.x;
-  const float* Hb = H + b * C * C + (g * kN) * C + g * kN;
+  const int64_t blk = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  if (blk >= B * G) return;  // whole wavefront
+  const int64_t b = blk / G, g = blk % G;
+  const int p = lane >> 3, q = lane & 7;
+  double* bc = bcast[wave];
 
+  // the lane's 4x4 tile of the undamped block (rows 4p+r, columns 4q+c)
+  float h[4][4];
+  {
+    const float* src = H + b * C * C + (g * kN + 4 * p) * C + g * kN + 4 * q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float4 v = *reinterpret_cast<const float4*>(src + r * C);
+      h[r][0] = v.x, h[r][1] = v.y, h[r][2] = v.z, h[r][3] = v.w;
+      if (Hc) *reinterpret_cast<float4*>(Hc + blk * kN * kN + (4 * p + r) * kN + 4 * q) = v;
+    }
+  }
   // diag mean (fp64 sum, rounded once) clamped like torch .clamp(min=1e-8)
-  double dsum = 0.0;
-  for (int i = 0; i < kN; ++i) dsum += static_cast<double>(Hb[static_cast<int64_t>(i) * C + i]);
-  float dmean = static_cast<float>(dsum / kN);
+  double ds = 0.0;
+  if (p == q) ds = (static_cast<double>(h[0][0]) + h[1][1]) + (static_cast<double>(h[2][2]) + h[3][3]);
+  float dmean = static_cast<float>(wave_sum_f64(ds) / kN);
   dmean = (dmean < 1e-8f) ? 1e-8f : dmean;  // NaN stays NaN
 
-  if (Hc) {
-    float* dst = Hc + (b * G + g) * kN * kN;
-    for (int e = lane; e < kN * kN; e += 64) dst[e] = Hb[static_cast<int64_t>(e / kN) * C + e % kN];
-  }
-  if (sym) {
-    bool same = true;
-    for (int e = lane; e < kN * kN; e += 64) {
-      const int i = e / kN, j = e % kN;
-      same = same && (__float_as_uint(Hb[static_cast<int64_t>(i) * C + j]) ==
-                      __float_as_uint(Hb[static_cast<int64_t>(j) * C + i]));
-    }
-    const bool all_same = __all(same);
-    if (lane == 0) sym[b * G + g] = all_same ? 1 : 0;
-  }
-
+  double R[4][4], piv[4];
   float cur = damp;
   int used = 0;
   for (int att = 1; att <= max_attempts; ++att) {
     const float lam = dmean * cur;
-    // Hd in fp32 (diag += lam), widened to fp64
-    for (int e = lane; e < kN * kN; e += 64) {
-      const int i = e / kN, j = e % kN;
-      float v = Hb[static_cast<int64_t>(i) * C + j];
-      if (i == j) v = v + lam;
-      A[i][j] = static_cast<double>(v);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int i = 4 * p + r, k = 4 * q + c;
+        const float v = (i == k) ? h[r][c] + lam : h[r][c];  // Hd in fp32
+        R[r][c] = (k <= i) ? static_cast<double>(v) : 0.0;
+      }
+      piv[r] = 0.0;
     }
-    __syncthreads();
     bool ok = true;
-    for (int j = kN - 1; j >= 0; --j) {
-      const double d = A[j][j];
-      if (!(d > 0.0)) {  // uniform: every lane reads the same pivot
-        ok = false;
-        break;
+    // j = 4 jp + jr: the row-group loop stays rolled (its predicates are
+    // computed per iteration), the 4 rows of a group are unrolled so that
+    // register indices are compile-time constants.
+#pragma unroll 1
+    for (int jp = kN / 4 - 1; jp >= 0; --jp) {
+      const bool own_row = (p == jp), own_col = (q == jp);
+#pragma unroll
+      for (int jr = 3; jr >= 0; --jr) {
+        const int j = 4 * jp + jr;
+        if (own_row) {  // the 8 lanes holding row j publish it
+          *reinterpret_cast<f64x2_t*>(bc + 4 * q) = f64x2_t{R[jr][0], R[jr][1]};
+          *reinterpret_cast<f64x2_t*>(bc + 4 * q + 2) = f64x2_t{R[jr][2], R[jr][3]};
+        }
+        __builtin_amdgcn_wave_barrier();
+        const f64x2_t a01 = *reinterpret_cast<const f64x2_t*>(bc + 4 * p);
+        const f64x2_t a23 = *reinterpret_cast<const f64x2_t*>(bc + 4 * p + 2);
+        const f64x2_t b01 = *reinterpret_cast<const f64x2_t*>(bc + 4 * q);
+        const f64x2_t b23 = *reinterpret_cast<const f64x2_t*>(bc + 4 * q + 2);
+        const double d = bc[j];
+        __builtin_amdgcn_wave_barrier();
+        ok = ok & (d > 0.0);
+        const double rd = recip_f64(d);
+        piv[jr] = own_row ? d : piv[jr];
+        const double ai[4] = {a01.x, a01.y, a23.x, a23.y};
+        const double ak[4] = {b01.x, b01.y, b23.x, b23.y};
+        double cf[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cf[r] = (4 * p + r < j) ? ai[r] * rd : 0.0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) R[r][c] = fma(-cf[r], ak[c], R[r][c]);
+          // column j of the inverse: X[i][j] = -c_i (cf is 0 for rows i >= j,
+          // whose entry the fma above left unchanged)
+          if (4 * p + r < j) R[r][jr] = own_col ? -cf[r] : R[r][jr];
+        }
       }
-      const double s = sqrt(d);
-      __syncthreads();
-      if (lane < j) A[lane][j] = A[lane][j] / s;
-      if (lane == 0) A[j][j] = s;
-      __syncthreads();
-      // trailing update of the leading j x j block, upper part:
-      // A[i][k] -= V[i][j] * V[k][j] for i <= k < j
-      const int i = lane & 31;
-      if (i < j) {
-        const double vi = A[i][j];
-        for (int k = i + (lane >> 5); k < j; k += 2) A[i][k] = A[i][k] - vi * A[k][j];
-      }
-      __syncthreads();
     }
-    if (ok) {
+    if (__builtin_amdgcn_readfirstlane(ok ? 1 : 0)) {  // d is the same in every lane
       used = att;
       break;
     }
     cur = cur * 10.0f;
-    __syncthreads();
   }
-  float* Ub = U + (b * G + g) * kN * kN;
+  float* Ub = U + blk * kN * kN;
   if (used == 0) {
-    for (int e = lane; e < kN * kN; e += 64) Ub[e] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float4*>(Ub + (4 * p + r) * kN + 4 * q) = float4{0.f, 0.f, 0.f, 0.f};
     if (lane == 0) attempts[g * B + b] = 0;
     return;
   }
-  // W = V^-1 (upper): lane j back-substitutes column j.
-  if (lane < kN) {
-    const int j = lane;
-    Wm[j][j] = 1.0 / A[j][j];
-    for (int i = j - 1; i >= 0; --i) {
-      double s = 0.0;
-      for (int k = i + 1; k <= j; ++k) s += A[i][k] * Wm[k][j];
-      Wm[i][j] = -s / A[i][i];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * p + r;
+    const double rs = 1.0 / sqrt(piv[r]);  // meaningful where the tile holds column i
+    float o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int k = 4 * q + c;
+      o[c] = (k > i) ? static_cast<float>(R[r][c] * rs) : (k == i ? static_cast<float>(rs) : 0.0f);
     }
-  }
-  __syncthreads();
-  for (int e = lane; e < kN * kN; e += 64) {
-    const int i = e / kN, j = e % kN;
-    Ub[e] = (i <= j) ? static_cast<float>(Wm[i][j]) : 0.0f;
+    *reinterpret_cast<float4*>(Ub + i * kN + 4 * q) = float4{o[0], o[1], o[2], o[3]};
   }
   if (lane == 0) attempts[g * B + b] = used;
 }
@@ -127,11 +178,11 @@ __global__ void __launch_bounds__(64)
 
 // Launch helper shared with the MXFP solver.
 int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, uint8_t* sym, float* Hc, hipStream_t s) {
-  const int64_t G = C / kN;
-  if (B * G == 0) return MGQ_OK;
-  hinv32_kernel<<<static_cast<unsigned>(B * G), 64, 0, s>>>(H, B, C, damp, max_attempts, U,
-                                                          attempts, sym, Hc);
+                  int32_t* attempts, float* Hc, hipStream_t s) {
+  const int64_t n = B * (C / kN);
+  if (n == 0) return MGQ_OK;
+  hinv32_kernel<<<static_cast<unsigned>((n + kWaves - 1) / kWaves), 64 * kWaves, 0, s>>>(
+      H, B, C, damp, max_attempts, U, attempts, Hc);
   return check_launch("hinv32");
 }
 
@@ -147,6 +198,7 @@ extern "C" int mgq_prepare_hinv_blocks(const float* H, int64_t B, int64_t C, int
   MGQ_REQUIRE(B >= 0 && C >= 0 && C % kN == 0, MGQ_ERR_SHAPE,
               "C=%lld not a multiple of the block size %d", (long long)C, kN);
   MGQ_REQUIRE(max_attempts >= 1, MGQ_ERR_VALUE, "max_attempts must be >= 1");
-  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, nullptr, nullptr,
-                       as_stream(stream));
+  MGQ_REQUIRE((reinterpret_cast<uintptr_t>(H) & 15u) == 0 && (reinterpret_cast<uintptr_t>(U) & 15u) == 0,
+              MGQ_ERR_SHAPE, "H and U must be 16-byte aligned");
+  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, nullptr, as_stream(stream));
 }

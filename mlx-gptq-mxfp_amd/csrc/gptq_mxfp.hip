@@ -31,7 +31,7 @@
 namespace mgq {
 
 int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, uint8_t* sym, float* Hc, hipStream_t s);
+                  int32_t* attempts, float* Hc, hipStream_t s);
 
 namespace {
 
@@ -240,7 +240,7 @@ template <typename TIn, bool IS_F16, int MODE, bool SAFE>
 __global__ void __launch_bounds__(kThreads)
     mxfp_solve_kernel(const TIn* __restrict__ W, int64_t B, int64_t R, int64_t C,
                       const float* __restrict__ Hc, const float* __restrict__ U,
-                      const uint8_t* __restrict__ dead, const uint8_t* __restrict__ symflag,
+                      const uint8_t* __restrict__ dead,
                       Offsets offs, uint8_t* __restrict__ q_out, uint8_t* __restrict__ s_out,
                       float* __restrict__ W_dq, double* __restrict__ rel_part) {
   const int64_t G = C / kG;
@@ -521,7 +521,7 @@ __global__ void rel_err_kernel(const double* __restrict__ part, int64_t n_per_b,
 }
 
 struct WsLayout {
-  int64_t dead_off, sym_off, u_off, hc_off, rel_off, total;
+  int64_t dead_off, u_off, hc_off, rel_off, total;
 };
 
 WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
@@ -529,8 +529,7 @@ WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
   const int64_t G = C / kG;
   WsLayout L;
   L.dead_off = 0;
-  L.sym_off = al(B * C);
-  L.u_off = L.sym_off + al(B * G);
+  L.u_off = al(B * C);
   L.hc_off = L.u_off + al(B * G * kG * kG * 4);
   L.rel_off = L.hc_off + al(B * G * kG * kG * 4);
   L.total = L.rel_off + al(B * G * ((R + 63) / 64) * 2 * 8);
@@ -539,14 +538,14 @@ WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
 
 template <typename TIn, bool IS_F16>
 int launch_solve(const void* W, int64_t B, int64_t R, int64_t C, const float* Hc, const float* U,
-                 const uint8_t* dead, const uint8_t* sym, int mode, bool safe, const Offsets& offs, uint8_t* q,
+                 const uint8_t* dead, int mode, bool safe, const Offsets& offs, uint8_t* q,
                  uint8_t* s, float* W_dq, double* rel_part, hipStream_t st) {
   const int64_t G = C / kG;
   const int64_t blocks = B * G * ((R + kThreads - 1) / kThreads);
   const TIn* w = static_cast<const TIn*>(W);
 #define MGQ_LAUNCH(MODE, SAFE)                                                              \
   mxfp_solve_kernel<TIn, IS_F16, MODE, SAFE><<<static_cast<unsigned>(blocks), kThreads, 0, st>>>( \
-      w, B, R, C, Hc, U, dead, sym, offs, q, s, W_dq, rel_part)
+      w, B, R, C, Hc, U, dead, offs, q, s, W_dq, rel_part)
   if (mode == kMxfp4) {
     if (safe) MGQ_LAUNCH(kMxfp4, true); else MGQ_LAUNCH(kMxfp4, false);
   } else {
@@ -596,31 +595,31 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
   MGQ_REQUIRE(rel_err == nullptr || static_cast<const void*>(W_dq) != W, MGQ_ERR_VALUE,
               "rel_err needs W_dq separate from W (in-place solves skip rel_err)");
   MGQ_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(H) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(W_dq) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0,
-              MGQ_ERR_SHAPE, "W, W_dq and q_out must be 16-byte aligned");
+              MGQ_ERR_SHAPE, "W, H, W_dq and q_out must be 16-byte aligned");
   if (B == 0 || C == 0) return MGQ_OK;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
   uint8_t* dead = reinterpret_cast<uint8_t*>(ws + L.dead_off);
-  uint8_t* sym = reinterpret_cast<uint8_t*>(ws + L.sym_off);
   float* U = reinterpret_cast<float*>(ws + L.u_off);
   float* Hcmp = reinterpret_cast<float*>(ws + L.hc_off);
   double* rel_part = reinterpret_cast<double*>(ws + L.rel_off);
 
   dead_fix_kernel<<<elementwise_blocks(B * C, 256), 256, 0, st>>>(H, B, C, dead);
   if (int rc = check_launch("dead-column fix")) return rc;
-  if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, sym, Hcmp, st)) return rc;
+  if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st)) return rc;
   if (R == 0) return MGQ_OK;
   int rc;
   if (w_dtype == kF32) {
-    rc = launch_solve<float, false>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<float, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
                                     scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else if (w_dtype == kBF16) {
-    rc = launch_solve<uint16_t, false>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<uint16_t, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
                                        scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else {
-    rc = launch_solve<uint16_t, true>(W, B, R, C, Hcmp, U, dead, sym, mode, algorithm == 1, offs, q_out,
+    rc = launch_solve<uint16_t, true>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
                                       scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   }
   if (rc) return rc;

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import logging
 
+import numpy as np
 import pytest
 import torch
 
@@ -97,6 +98,30 @@ def test_prepare_hinv_blocks_vs_oracle():
     assert torch.equal(U, U.triu())
     rel = (U - Ur).norm(dim=(1, 2)) / Ur.norm(dim=(1, 2))
     assert float(rel.max()) < 1e-4
+
+
+def test_prepare_hinv_blocks_fp64_rounded_and_lower_triangle():
+    """U against the float64 factor of (Hd)^-1 rounded once: every entry within
+    one fp32 rounding. The upper triangle of H carries junk that
+    torch.linalg.cholesky_ex (the reference's factorisation, gptq.py:39)
+    never reads, so the result must not depend on it."""
+    from mlx_gptq import gptq
+
+    g = torch.Generator().manual_seed(11)
+    A = torch.randn(48, 32, 80, generator=g) * torch.exp(torch.randn(48, 32, 1, generator=g))
+    H = (A @ A.transpose(1, 2)).float()
+    junk = H + torch.triu(torch.randn(48, 32, 32, generator=g), 1) * H.abs().amax(dim=(1, 2), keepdim=True)
+    U = gptq._prepare_hinv(junk.to(DEV), 0.01).cpu().double().numpy()
+    Hn = H.numpy()
+    for b in range(48):
+        d = np.float32(np.diagonal(Hn[b]).astype(np.float64).sum() / 32)
+        lam = np.float32(max(d, np.float32(1e-8)) * np.float32(0.01))
+        Hd = Hn[b].copy()
+        Hd[np.arange(32), np.arange(32)] += lam  # fp32 add, as the reference
+        Hs = np.tril(Hd).astype(np.float64)
+        Hs = Hs + np.tril(Hs, -1).T
+        Uref = np.linalg.cholesky(np.linalg.inv(Hs)).T
+        assert np.all(np.abs(U[b] - Uref) <= 1.2e-7 * np.abs(Uref) + 1e-9 * np.abs(Uref).max()), b
 
 
 def test_escalation_warnings_and_failure_match_reference(caplog):
