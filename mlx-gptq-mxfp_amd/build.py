@@ -22,6 +22,10 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 OUT = HERE / "mlx_gptq" / "libmlxgptq_hip.so"
 ARCH = "gfx950"
+# Test-only GPU library: the exhaustive check of the hardware MX conversion
+# forms (csrc/mx_hw.h) that tests/test_gpu_mx_hw.py runs.
+HWCHECK_SRC = HERE.parent / "tests" / "native" / "check_mx_hw.hip"
+HWCHECK_OUT = HERE.parent / "tests" / "native" / "libmgq_hwcheck.so"
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -81,7 +85,20 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, OUT)
+    if HWCHECK_SRC.exists():
+        _build_hwcheck(verbose)
     return OUT
+
+
+def _build_hwcheck(verbose: bool) -> None:
+    tmp = HWCHECK_OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), *COMMON_FLAGS, "-shared", "-I", str(CSRC), str(HWCHECK_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {HWCHECK_SRC.name}:\n{res.stderr}")
+    os.replace(tmp, HWCHECK_OUT)
 
 
 def main(argv: list[str] | None = None) -> int:

@@ -27,6 +27,7 @@
 
 #include "mgq_capi.h"
 #include "mgq_common.h"
+#include "mx_hw.h"
 
 namespace mgq {
 
@@ -60,32 +61,24 @@ __global__ void dead_fix_kernel(float* __restrict__ H, int64_t B, int64_t C,
 }
 
 // Exact reference projection of one element (code and dq), w / scale done
-// as w * inv_scale (identical for power-of-two scales).
+// as w * inv_scale (identical for power-of-two scales), on the hardware MX
+// conversions.
 template <int MODE>
 __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, float* dq) {
-  const float n = w * inv_scale;
-  uint32_t code;
-  float v;
-  if (MODE == kMxfp4) {
-    return mx4_encode(w, inv_scale, scale, dq);
-  } else {
-    code = e4m3_code_clamped(clamp448(n));
-    v = e4m3_value(code);
-  }
-  *dq = v * scale;
-  return code;
+  if constexpr (MODE == kMxfp4)
+    return mx4_encode_hw(w, inv_scale, scale, dq);
+  else
+    return mx8_encode_hw(w, inv_scale, scale, dq);
 }
 
-// (dq - w) / scale for scoring a scale candidate (quant_exact's dq minus w,
-// in units of the scale, without materialising the code).
+// (dq - w) / scale of two weights for scoring a scale candidate.
 template <int MODE>
-__device__ inline float quant_err(float w, float inv_scale) {
-  if constexpr (MODE == kMxfp4) {
-    return mx4_err(w, inv_scale);
-  } else {
-    const float n = w * inv_scale;
-    return e4m3_round(n) - n;
-  }
+__device__ inline void quant_err2(float w0, float w1, float scale, float inv_scale, float lim,
+                                  float& e0, float& e1) {
+  if constexpr (MODE == kMxfp4)
+    mx4_cand_err2(w0, w1, scale, inv_scale, e0, e1);
+  else
+    mx8_cand_err2(w0, w1, scale, inv_scale, lim, e0, e1);
 }
 
 // e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
@@ -181,6 +174,42 @@ __device__ inline float mfma_objective(const float (&e)[kG], const HOperand& A) 
   return obj;
 }
 
+// The same objective when every e[c] is exactly a bf16 value (bf16 weights
+// and candidate scales whose |w / scale| stays below 512 for MXFP4, 16384
+// for MXFP8): E is one exact bf16 operand, so the hi*lo products of
+// mfma_objective are zero and are skipped. The non-zero products are
+// accumulated in the same order, so both functions return the same bits for
+// the same errors.
+__device__ inline float mfma_objective_x1(const float (&e)[kG], const HOperand& A) {
+  f32x16_t d0, d1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d0[r] = d1[r] = 0.0f;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    bf16x8_t x, y;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x[j] = static_cast<__bf16>(e[16 * kc + j]);
+      y[j] = static_cast<__bf16>(e[16 * kc + 8 + j]);
+    }
+    swap_halves(x, y);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], x, d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], y, d1, 0, 0, 0);
+    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], x, d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], y, d1, 0, 0, 0);
+  }
+  float obj = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d0[r]), __float_as_uint(d1[r]),
+                                                     false, false);
+    const int c0 = 8 * (r >> 2) + (r & 3);
+    obj = fmaf(e[c0], __uint_as_float(sw[0]), obj);
+    obj = fmaf(e[c0 + 4], __uint_as_float(sw[1]), obj);
+  }
+  return obj;
+}
+
 // An opaque zero that depends on `v`: addresses built from it cannot be
 // computed before `v`, so the loads behind them are neither hoisted out of
 // the loop nor scheduled far ahead of their use (without this the compiler
@@ -236,13 +265,16 @@ __device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float
   }
 }
 
-template <typename TIn, bool IS_F16, int MODE, bool SAFE>
+// XERR: the candidate errors are exact in bf16 (bf16 weights, offsets within
+// the bound the host checks), so their objective uses mfma_objective_x1.
+template <typename TIn, bool IS_F16, int MODE, bool SAFE, bool XERR>
 __global__ void __launch_bounds__(kThreads)
     mxfp_solve_kernel(const TIn* __restrict__ W, int64_t B, int64_t R, int64_t C,
                       const float* __restrict__ Hc, const float* __restrict__ U,
                       const uint8_t* __restrict__ dead,
                       Offsets offs, uint8_t* __restrict__ q_out, uint8_t* __restrict__ s_out,
                       float* __restrict__ W_dq, double* __restrict__ rel_part) {
+  static_assert(!XERR || (SAFE && sizeof(TIn) == 2 && !IS_F16), "XERR needs bf16 weights");
   const int64_t G = C / kG;
   const int64_t chunks = (R + kThreads - 1) / kThreads;
   const int64_t bg = blockIdx.x / chunks;
@@ -267,13 +299,16 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t base = (b * R + r) * C + g * kG;
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
 
-  // The group's 32 (dead-column-fixed) weights live in LDS, one column per
-  // thread (so[i][tid]: conflict-free), not in registers, which leaves room
-  // for 3 waves per SIMD without spills. 16-bit inputs are kept as their own
-  // bits (exact), which halves the array.
-  using OrigT = std::conditional_t<sizeof(TIn) == 2, uint16_t, float>;
-  __shared__ OrigT so[kG * kThreads];
+  // The group's 32 (dead-column-fixed) weights live in LDS as fp32, not in
+  // registers, which leaves room for 3 waves per SIMD without spills.
+  // Weights 2p and 2p+1 of thread t sit side by side at
+  // so[p * 2 kThreads + 2t], so a pair is one 8-byte read and both pair and
+  // single reads are conflict-free.
+  __shared__ float so[kG * kThreads];
   float amax;
+  // rel_err partials (gptq.py:300-302) against the caller's W as given:
+  // den = sum w^2 and, for dead columns (whose W_dq is 0), their w^2.
+  float den = 0.0f, dead_sq = 0.0f;
   {
     float v[kG];
     load_group<TIn, IS_F16>(W, base, v);
@@ -281,6 +316,15 @@ __global__ void __launch_bounds__(kThreads)
     const uint4 m0 = reinterpret_cast<const uint4*>(dd)[0];
     const uint4 m1 = reinterpret_cast<const uint4*>(dd)[1];
     const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    if (rel_part) {
+#pragma unroll
+      for (int i = 0; i < kG; ++i) den = fmaf(v[i], v[i], den);
+      if ((m0.x | m0.y | m0.z | m0.w | m1.x | m1.y | m1.z | m1.w) != 0u) {  // uniform
+#pragma unroll
+        for (int i = 0; i < kG; ++i)
+          if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) dead_sq = fmaf(v[i], v[i], dead_sq);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kG; ++i)
       if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) v[i] = 0.0f;
@@ -288,52 +332,50 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(v[i]));
 #pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      if constexpr (sizeof(TIn) == 4)
-        so[i * kThreads + threadIdx.x] = v[i];
-      else if constexpr (IS_F16)
-        so[i * kThreads + threadIdx.x] = f32_to_f16_rne(v[i]);
-      else
-        so[i * kThreads + threadIdx.x] = static_cast<uint16_t>(f2u(v[i]) >> 16);
-    }
+    for (int p = 0; p < kG / 2; ++p)
+      *reinterpret_cast<float2*>(so + p * 2 * kThreads + 2 * threadIdx.x) = make_float2(v[2 * p], v[2 * p + 1]);
   }
-  const OrigT* orig = so + threadIdx.x;  // orig[i * kThreads] = weight i
-  auto orig_at = [](const OrigT* p, int i) __attribute__((always_inline)) -> float {
-    if constexpr (sizeof(TIn) == 4)
-      return p[i * kThreads];
-    else if constexpr (IS_F16)
-      return f16_to_f32(p[i * kThreads]);
-    else
-      return bf16_to_f32(p[i * kThreads]);
+  const float* orig = so + 2 * threadIdx.x;
+  // weights 2p and 2p+1
+  auto orig_pair = [](const float* o, int p, float& a, float& c) __attribute__((always_inline)) {
+    const float2 x = *reinterpret_cast<const float2*>(o + p * 2 * kThreads);
+    a = x.x;
+    c = x.y;
+  };
+  auto orig_at = [](const float* o, int i) __attribute__((always_inline)) -> float {
+    return o[(i / 2) * 2 * kThreads + (i & 1)];
   };
 #define ORIG(i) orig_at(orig, (i))
-  // The dequantized values of the selected result: in LDS (same layout)
-  // for the safe search, whose candidate objectives need the registers; in
-  // registers for the groupwise solve, which keeps that kernel's LDS small.
-  // MXFP4 values (at most 2 significant bits times a power of two >= 2^-128)
-  // are exact in bf16, so they are stored as the top half of their fp32 bits.
-  using DqT = std::conditional_t<MODE == kMxfp4, uint16_t, float>;
+  // The dequantized values of the selected result: in LDS for the safe
+  // search, whose candidate objectives need the registers; in registers for
+  // the groupwise solve. MXFP4 values (at most 2 significant bits times a
+  // power of two >= 2^-128) are exact in bf16 and are stored as the top half
+  // of their fp32 bits; MXFP8 stores the E4M3 code and decodes it on read
+  // (value(code) * scale, what the encoder returned).
+  using DqT = std::conditional_t<MODE == kMxfp4, uint16_t, uint8_t>;
   float dqr[SAFE ? 1 : kG];
   DqT* dqs = nullptr;
   if constexpr (SAFE) {
     __shared__ DqT sdq[kG * kThreads];
     dqs = sdq + threadIdx.x;
   }
+  float dq_scale = 0.0f;  // the selected scale, set before the first read
   auto dq_get = [&](int i) __attribute__((always_inline)) -> float {
     if constexpr (!SAFE)
       return dqr[i];
     else if constexpr (MODE == kMxfp4)
       return bf16_to_f32(dqs[i * kThreads]);
     else
-      return dqs[i * kThreads];
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(static_cast<uint32_t>(dqs[i * kThreads]), 1.0f,
+                                                      false)[0] * dq_scale;
   };
-  auto dq_set = [&](int i, float v) __attribute__((always_inline)) {
+  auto dq_set = [&](int i, float v, uint32_t code) __attribute__((always_inline)) {
     if constexpr (!SAFE)
       dqr[i] = v;
     else if constexpr (MODE == kMxfp4)
       dqs[i * kThreads] = static_cast<uint16_t>(f2u(v) >> 16);
     else
-      dqs[i * kThreads] = v;
+      dqs[i * kThreads] = static_cast<uint8_t>(code);
   };
 #define DQ(i) dq_get(i)
 
@@ -350,22 +392,25 @@ __global__ void __launch_bounds__(kThreads)
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
       e = e < -127 ? -127 : (e > 127 ? 127 : e);
-      const float inv = exp2_int(-e);
+      const float inv = exp2_int(-e), sc = exp2_int(e);
+      const float lim = (MODE == kMxfp8) ? mx8_clamp_limit(sc) : 0.0f;
       // re-read the weights from LDS per candidate (an opaque offset keeps
       // the compiler from holding all 32 in registers across the loop)
-      const OrigT* og = orig + zero_after(inv);
-      // eight elements at a time: the scheduler would otherwise run each op
+      const float* og = orig + zero_after(inv);
+      // four pairs at a time: the scheduler would otherwise run each op
       // over all 32 elements before the next and hold 4 x 32 temporaries
 #pragma unroll
-      for (int i0 = 0; i0 < kG; i0 += 8) {
+      for (int p0 = 0; p0 < kG / 2; p0 += 4) {
 #pragma unroll
-        for (int i = i0; i < i0 + 8; ++i) {
-          const float x = orig_at(og, i);
-          err[i] = quant_err<MODE>(x, inv);
+        for (int p = p0; p < p0 + 4; ++p) {
+          float a, c;
+          orig_pair(og, p, a, c);
+          quant_err2<MODE>(a, c, sc, inv, lim, err[2 * p], err[2 * p + 1]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      const float obj = mfma_objective(err, Ah) * exp2_int(2 * (e - e0));
+      const float raw = XERR ? mfma_objective_x1(err, Ah) : mfma_objective(err, Ah);
+      const float obj = raw * exp2_int(2 * (e - e0));
       if (o == 0 || obj < best) {
         best = obj;
         e_sel = e;
@@ -373,6 +418,7 @@ __global__ void __launch_bounds__(kThreads)
     }
   }
   const float scale = exp2_int(e_sel), inv_scale = exp2_int(-e_sel);
+  dq_scale = scale;
 
   // 2. GPTQ recurrence with the fixed scale, column by column. The
   // reference updates all later columns after each step
@@ -401,7 +447,7 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
     errs[c] = (acc - dq) / col[c];
     codes[c / 4] |= code << (8 * (c % 4));
-    dq_set(c, dq);
+    dq_set(c, dq, code);
   }
 
   // 3. GPTQ vs best RTN candidate (safe search only)
@@ -436,14 +482,14 @@ __global__ void __launch_bounds__(kThreads)
       float dq;
       const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
       codes[i / 4] |= code << (8 * (i % 4));
-      dq_set(i, dq);
+      dq_set(i, dq, code);
     }
   }
   float w[kG];
 #pragma unroll
   for (int i = 0; i < kG; ++i) w[i] = DQ(i);
 
-  double num = 0.0, den = 0.0;
+  double num = 0.0, den_d = 0.0;
   if (valid) {
     uint4* qp = reinterpret_cast<uint4*>(q_out + base);
     qp[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
@@ -454,20 +500,16 @@ __global__ void __launch_bounds__(kThreads)
       op[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
     s_out[(b * R + r) * G + g] = static_cast<uint8_t>(e_sel + 127);
     if (rel_part) {
-      // rel_err against the caller's W as given, dead columns included
-      // (gptq.py:300-302). W does not alias W_dq when rel_err is requested
-      // (checked on the host), so re-reading it here is safe and keeps 32
-      // registers free during the solve.
-      float raw[kG];
-      // opaque offset: a fresh load after the solve, not the first load's
-      // registers kept alive through it
-      load_group<TIn, IS_F16>(W, base + zero_after(w[kG - 1]), raw);
+      // live columns: (W_dq - w)^2 from the LDS copy (dead columns hold 0
+      // there and in W_dq; their w^2 is dead_sq)
+      float sq = dead_sq;
 #pragma unroll
       for (int i = 0; i < kG; ++i) {
-        const double d = static_cast<double>(w[i]) - static_cast<double>(raw[i]);
-        num += d * d;
-        den += static_cast<double>(raw[i]) * static_cast<double>(raw[i]);
+        const float d = w[i] - ORIG(i);
+        sq = fmaf(d, d, sq);
       }
+      num = sq;
+      den_d = den;
     }
   }
   if (rel_part) {
@@ -475,7 +517,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       num += __shfl_xor(num, off);
-      den += __shfl_xor(den, off);
+      den_d += __shfl_xor(den_d, off);
     }
     if ((threadIdx.x & 63) == 0) {
       const int64_t waves = (R + 63) / 64;
@@ -483,7 +525,7 @@ __global__ void __launch_bounds__(kThreads)
       if (wv < waves) {
         double* pp = rel_part + ((b * G + g) * waves + wv) * 2;
         pp[0] = num;
-        pp[1] = den;
+        pp[1] = den_d;
       }
     }
   }
@@ -536,20 +578,22 @@ WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
   return L;
 }
 
-template <typename TIn, bool IS_F16>
+template <typename TIn, bool IS_F16, bool XERR>
 int launch_solve(const void* W, int64_t B, int64_t R, int64_t C, const float* Hc, const float* U,
                  const uint8_t* dead, int mode, bool safe, const Offsets& offs, uint8_t* q,
                  uint8_t* s, float* W_dq, double* rel_part, hipStream_t st) {
   const int64_t G = C / kG;
   const int64_t blocks = B * G * ((R + kThreads - 1) / kThreads);
   const TIn* w = static_cast<const TIn*>(W);
-#define MGQ_LAUNCH(MODE, SAFE)                                                              \
-  mxfp_solve_kernel<TIn, IS_F16, MODE, SAFE><<<static_cast<unsigned>(blocks), kThreads, 0, st>>>( \
+#define MGQ_LAUNCH(MODE, SAFE, X)                                                                    \
+  mxfp_solve_kernel<TIn, IS_F16, MODE, SAFE, X><<<static_cast<unsigned>(blocks), kThreads, 0, st>>>( \
       w, B, R, C, Hc, U, dead, offs, q, s, W_dq, rel_part)
-  if (mode == kMxfp4) {
-    if (safe) MGQ_LAUNCH(kMxfp4, true); else MGQ_LAUNCH(kMxfp4, false);
+  if constexpr (XERR) {
+    if (mode == kMxfp4) MGQ_LAUNCH(kMxfp4, true, true); else MGQ_LAUNCH(kMxfp8, true, true);
+  } else if (mode == kMxfp4) {
+    if (safe) MGQ_LAUNCH(kMxfp4, true, false); else MGQ_LAUNCH(kMxfp4, false, false);
   } else {
-    if (safe) MGQ_LAUNCH(kMxfp8, true); else MGQ_LAUNCH(kMxfp8, false);
+    if (safe) MGQ_LAUNCH(kMxfp8, true, false); else MGQ_LAUNCH(kMxfp8, false, false);
   }
 #undef MGQ_LAUNCH
   return check_launch("mxfp solve");
@@ -611,16 +655,26 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
   if (int rc = check_launch("dead-column fix")) return rc;
   if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st)) return rc;
   if (R == 0) return MGQ_OK;
+  // Candidate errors are exact in bf16 for bf16 weights while every
+  // |w / scale| stays below 512 (MXFP4) or 16384 (MXFP8): with e0 the
+  // groupwise exponent, |w / 2^(e0+off)| <= fmax * 2^(0.5 - off), so offsets
+  // >= -5 (MXFP4) or >= -4 (MXFP8) keep it there.
+  int min_off = 0;
+  for (int i = 0; i < offs.n; ++i) min_off = offs.v[i] < min_off ? offs.v[i] : min_off;
+  const bool xerr = algorithm == 1 && w_dtype == kBF16 && min_off >= (mode == kMxfp4 ? -5 : -4);
   int rc;
   if (w_dtype == kF32) {
-    rc = launch_solve<float, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
-                                    scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<float, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
+                                           scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+  } else if (w_dtype == kBF16 && xerr) {
+    rc = launch_solve<uint16_t, false, true>(W, B, R, C, Hcmp, U, dead, mode, true, offs, q_out,
+                                             scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else if (w_dtype == kBF16) {
-    rc = launch_solve<uint16_t, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
-                                       scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<uint16_t, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs,
+                                              q_out, scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   } else {
-    rc = launch_solve<uint16_t, true>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
-                                      scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<uint16_t, true, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
+                                             scales_out, W_dq, rel_err ? rel_part : nullptr, st);
   }
   if (rc) return rc;
   if (rel_err) {

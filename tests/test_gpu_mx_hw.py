@@ -1,0 +1,44 @@
+"""The solver's MXFP element arithmetic on gfx950's scaled MX conversion
+instructions (csrc/mx_hw.h), checked on the GPU for every fp32 weight at a
+spread of scale exponents against the exact software encoders of
+csrc/mgq_common.h (themselves pinned to the reference's threshold chain,
+grid.py:82-105, by tests/test_mx4_projection.py, and to torch's float8_e4m3fn
+cast by the encoder tests):
+
+- codes and dq of the recurrence's encoders: bit-exact;
+- candidate errors (q - n) used to score scale candidates: bit-exact except
+  where n = w / scale is below 2^-126 in magnitude, where both are below it;
+- for bf16 weights those errors are exact in bf16 whenever
+  2^-126 <= |n| < 512 (MXFP4) or < 16384 (MXFP8), which is what lets the
+  candidate objective take them as a single bf16 MFMA operand.
+
+The library is built by build() from tests/native/check_mx_hw.hip.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "libmgq_hwcheck.so")
+KINDS = ["mx4 code", "mx4 dq", "mx8 code", "mx8 dq", "mx4 cand err", "mx8 cand err",
+         "mx4 err not bf16", "mx8 err not bf16"]
+
+
+@pytest.mark.parametrize("e", [-127, -126, -125, -64, -9, -1, 0, 1, 7, 64, 119, 120, 126, 127])
+def test_hw_mx_conversions_exhaustive(e):
+    import torch
+
+    assert torch.cuda.is_available()
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} missing: run build() first")
+    lib = ctypes.CDLL(LIB)
+    lib.mgq_hwcheck_mx.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_ulonglong)]
+    counts = (ctypes.c_ulonglong * 8)()
+    assert lib.mgq_hwcheck_mx(e, counts) == 0
+    bad = {k: int(c) for k, c in zip(KINDS, counts) if c}
+    assert not bad, (e, bad)
