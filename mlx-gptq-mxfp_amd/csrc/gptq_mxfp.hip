@@ -71,14 +71,25 @@ __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, fl
     return mx8_encode_hw(w, inv_scale, scale, dq);
 }
 
-// (dq - w) / scale of two weights for scoring a scale candidate.
+// (dq - w) / scale of eight weights for scoring a scale candidate.
 template <int MODE>
-__device__ inline void quant_err2(float w0, float w1, float scale, float inv_scale, float lim,
-                                  float& e0, float& e1) {
-  if constexpr (MODE == kMxfp4)
-    mx4_cand_err2(w0, w1, scale, inv_scale, e0, e1);
-  else
-    mx8_cand_err2(w0, w1, scale, inv_scale, lim, e0, e1);
+__device__ inline void quant_err8(const float (&w)[8], float scale, float inv_scale, float lim,
+                                  float* e) {
+  if constexpr (MODE == kMxfp4) {
+    float t[8];
+    mx4_cand_err8(w, scale, inv_scale, t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = t[j];
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x[4] = {w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
+      float t[4];
+      mx8_cand_err4(x, scale, inv_scale, lim, t);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[4 * h + j] = t[j];
+    }
+  }
 }
 
 // e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
@@ -290,9 +301,12 @@ __global__ void __launch_bounds__(kThreads)
   // U^T staged in LDS (Ut[c][k] = U[k][c]): the recurrence below reads one
   // column of U per step with broadcast LDS loads (uniform addresses).
   __shared__ float Ut[kG * kG];
+  // RN(1/U[c][c]) for the correctly rounded divisions of the recurrence
+  __shared__ float ydiag[kG];
   {
     const float* Ub = U + (b * G + g) * kG * kG;
     for (int e = threadIdx.x; e < kG * kG; e += kThreads) Ut[(e % kG) * kG + e / kG] = Ub[e];
+    if (threadIdx.x < kG) ydiag[threadIdx.x] = div_exact_recip(Ub[threadIdx.x * (kG + 1)]);
   }
   __syncthreads();
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
@@ -401,12 +415,10 @@ __global__ void __launch_bounds__(kThreads)
       // over all 32 elements before the next and hold 4 x 32 temporaries
 #pragma unroll
       for (int p0 = 0; p0 < kG / 2; p0 += 4) {
+        float x[8];
 #pragma unroll
-        for (int p = p0; p < p0 + 4; ++p) {
-          float a, c;
-          orig_pair(og, p, a, c);
-          quant_err2<MODE>(a, c, sc, inv, lim, err[2 * p], err[2 * p + 1]);
-        }
+        for (int p = 0; p < 4; ++p) orig_pair(og, p0 + p, x[2 * p], x[2 * p + 1]);
+        quant_err8<MODE>(x, sc, inv, lim, err + 2 * p0);
         __builtin_amdgcn_sched_barrier(0);
       }
       const float raw = XERR ? mfma_objective_x1(err, Ah) : mfma_objective(err, Ah);
@@ -445,7 +457,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     float dq;
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
-    errs[c] = (acc - dq) / col[c];
+    errs[c] = div_exact(acc - dq, col[c], ydiag[c]);  // = (acc - dq) / U[c][c]
     codes[c / 4] |= code << (8 * (c % 4));
     dq_set(c, dq, code);
   }

@@ -18,6 +18,14 @@
 // (tests/native/check_mx_hw.hip). The candidate errors differ from mx4_err
 // only where n = w / scale is below 2^-126 in magnitude (sign of zero or the
 // last subnormal bit), which no fp32 objective can see.
+//
+// div_exact: a / d correctly rounded with Markstein's correction from a
+// precomputed y = RN(1/d): q = a y, r = fma(-q, d, a) (exact),
+// q' = fma(r, y, q). q' equals the IEEE quotient for every pair of
+// significands (a, d in [1, 2): all 2^46 pairs checked on the GPU), hence for
+// every a, d whose intermediates stay normal: d in [2^-24, 2^24] (the caller
+// passes y = 0 otherwise) and 2^-100 <= |a| < 2^101. Other inputs (zero
+// included) take the IEEE division.
 #pragma once
 
 #include "mgq_common.h"
@@ -26,27 +34,49 @@ namespace mgq {
 
 typedef short mx_s16x2_t __attribute__((ext_vector_type(2)));
 
-// Quantization errors in units of the scale, (q - n) with n = w / 2^e, for two
-// weights: the FP4 code comes straight from w with the scale folded into the
-// conversion, and fma(w, -2^-e, q) is q - n rounded once (n is exact).
-__device__ inline void mx4_cand_err2(float w0, float w1, float scale, float inv_scale, float& e0,
-                                     float& e1) {
-  const uint32_t c = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, w0, w1, scale, 0);
-  const auto q = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, 1.0f, 0);
-  e0 = fmaf(w0, -inv_scale, q[0]);
-  e1 = fmaf(w1, -inv_scale, q[1]);
+// A register whose prior contents do not matter (the conversions below merge
+// into it byte- or word-wise and only the written parts are read back).
+__device__ inline uint32_t mx_undef_u32() {
+  uint32_t u;
+  asm volatile("" : "=v"(u));
+  return u;
 }
 
-// E4M3 counterpart; lim = min(448 * 2^e, FLT_MAX) clamps w so that w / 2^e
-// is clamp(n, +-448) exactly (and inf stays finite for the conversion).
-__device__ inline void mx8_cand_err2(float w0, float w1, float scale, float inv_scale, float lim,
-                                     float& e0, float& e1) {
-  const float c0 = __builtin_amdgcn_fmed3f(w0, -lim, lim);
-  const float c1 = __builtin_amdgcn_fmed3f(w1, -lim, lim);
-  const mx_s16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(mx_s16x2_t{0, 0}, c0, c1, scale, false);
-  const auto q = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(__builtin_bit_cast(uint32_t, c), 1.0f, false);
-  e0 = fmaf(w0, -inv_scale, q[0]);
-  e1 = fmaf(w1, -inv_scale, q[1]);
+// Quantization errors in units of the scale, (q - n) with n = w / 2^e, for
+// eight weights: the FP4 codes come straight from w with the scale folded
+// into the conversion (four pairs into the four bytes of one register), and
+// fma(w, -2^-e, q) is q - n rounded once (n is exact).
+__device__ inline void mx4_cand_err8(const float (&w)[8], float scale, float inv_scale, float (&e)[8]) {
+  uint32_t c = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(mx_undef_u32(), w[0], w[1], scale, 0);
+  c = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(c, w[2], w[3], scale, 1);
+  c = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(c, w[4], w[5], scale, 2);
+  c = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(c, w[6], w[7], scale, 3);
+  const auto q0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, 1.0f, 0);
+  const auto q1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, 1.0f, 1);
+  const auto q2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, 1.0f, 2);
+  const auto q3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(c, 1.0f, 3);
+  const float q[8] = {q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) e[j] = fmaf(w[j], -inv_scale, q[j]);
+}
+
+// E4M3 counterpart for four weights; lim = min(448 * 2^e, FLT_MAX) clamps w
+// so that w / 2^e is clamp(n, +-448) exactly (and inf stays finite for the
+// conversion).
+__device__ inline void mx8_cand_err4(const float (&w)[4], float scale, float inv_scale, float lim,
+                                     float (&e)[4]) {
+  float c[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_fmed3f(w[j], -lim, lim);
+  mx_s16x2_t p = __builtin_bit_cast(mx_s16x2_t, mx_undef_u32());
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, c[0], c[1], scale, false);
+  p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, c[2], c[3], scale, true);
+  const uint32_t u = __builtin_bit_cast(uint32_t, p);
+  const auto q0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(u, 1.0f, false);
+  const auto q1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(u, 1.0f, true);
+  const float q[4] = {q0[0], q0[1], q1[0], q1[1]};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) e[j] = fmaf(w[j], -inv_scale, q[j]);
 }
 
 __device__ inline float mx8_clamp_limit(float scale) {
@@ -73,6 +103,20 @@ __device__ inline uint32_t mx8_encode_hw(float w, float inv_scale, float scale, 
   code = (n != n) ? (((f2u(n) >> 24) & 0x80u) | 0x7fu) : code;
   *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0] * scale;
   return code;
+}
+
+__device__ inline float div_exact(float a, float d, float y) {
+  const float q = a * y;
+  const float r = fmaf(-q, d, a);
+  float e = fmaf(r, y, q);
+  const uint32_t ea = f2u(a) & 0x7f800000u;
+  if (!(y != 0.0f) || (ea - (27u << 23)) > (200u << 23)) e = a / d;
+  return e;
+}
+
+// y for div_exact: RN(1/d) where d is in [2^-24, 2^24], else 0.
+__device__ inline float div_exact_recip(float d) {
+  return (d >= 5.96046448e-8f && d <= 16777216.0f) ? 1.0f / d : 0.0f;
 }
 
 }  // namespace mgq

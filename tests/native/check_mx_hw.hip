@@ -1,20 +1,29 @@
-// Exhaustive GPU check of the solver's hardware MX conversion forms
-// (csrc/mx_hw.h) against the exact software encoders (csrc/mgq_common.h,
-// which tests/native/check_mx4_projection.hip pins against the threshold
-// chain of grid.py:82-105), for every fp32 weight w at one scale exponent e.
+// GPU checks of the solver's hardware-instruction arithmetic (csrc/mx_hw.h)
+// against the exact software forms (csrc/mgq_common.h, which
+// tests/native/check_mx4_projection.hip pins against the threshold chain of
+// grid.py:82-105) and against IEEE division.
 //
-// counts[k] after mgq_hwcheck_mx(e, counts):
+// mgq_hwcheck_mx(e, counts): every fp32 weight w at scale exponent e;
+// counts[k]:
 //   0  mx4_encode_hw code != mx4_encode code
 //   1  mx4_encode_hw dq   != mx4_encode dq           (bits; NaN == NaN)
 //   2  mx8_encode_hw code != e4m3_code_clamped(clamp448(n))
 //   3  mx8_encode_hw dq   != e4m3_value(code) * scale (bits; NaN == NaN)
-//   4  mx4_cand_err2      != mx4_err                  (bits, NaN == NaN; both
+//   4  mx4_cand_err8      != mx4_err                  (bits, NaN == NaN; both
 //                                                      below 2^-126 when n is)
-//   5  mx8_cand_err2      != e4m3_round(n) - n        (same rule)
+//   5  mx8_cand_err4      != e4m3_round(n) - n        (same rule)
 //   6  MXFP4 error not exact in bf16 although w is a bf16 value and
 //      2^-126 <= |n| < 512
 //   7  MXFP8 error not exact in bf16 although w is a bf16 value and
 //      2^-126 <= |n| < 16384
+//
+// mgq_hwcheck_div(stride_log, counts): div_exact(a, d, div_exact_recip(d))
+// against a / d, bit for bit:
+//   counts[0]: a, d over all significands in [1, 2), d every 2^stride_log-th
+//              (stride_log = 0: all 2^46 pairs);
+//   counts[1]: 2^12 pseudo-random significand pairs at every exponent pair
+//              ea in [-130, 127], ed in [-30, 30] (both guards' edges and
+//              the fallback side), signs mixed, plus a = 0.
 #include <hip/hip_runtime.h>
 
 #include "mx_hw.h"
@@ -33,17 +42,26 @@ __global__ void check_kernel(int e, unsigned long long* counts) {
   unsigned loc[kKinds] = {};
   const float inv = exp2_int(-e), scale = exp2_int(e);
   const float lim = mx8_clamp_limit(scale);
-  // 2^24 threads x 128 iterations x 2 weights = 2^32 inputs
+  // 2^22 threads x 128 iterations x 8 consecutive weights = 2^32 inputs
   for (int it = 0; it < 128; ++it) {
-    const unsigned long long t = static_cast<unsigned long long>(it) * (1ull << 24) +
+    const unsigned long long t = static_cast<unsigned long long>(it) * (1ull << 22) +
                                  static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint32_t u0 = static_cast<uint32_t>(2ull * t);
-    const float w[2] = {u2f(u0), u2f(u0 + 1u)};
-    float e4[2], e8[2];
-    mx4_cand_err2(w[0], w[1], scale, inv, e4[0], e4[1]);
-    mx8_cand_err2(w[0], w[1], scale, inv, lim, e8[0], e8[1]);
+    const uint32_t u0 = static_cast<uint32_t>(8ull * t);
+    float w[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 8; ++j) w[j] = u2f(u0 + j);
+    float e4[8], e8[8];
+    mx4_cand_err8(w, scale, inv, e4);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x[4] = {w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
+      float t8[4];
+      mx8_cand_err4(x, scale, inv, lim, t8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e8[4 * h + j] = t8[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
       const float n = w[j] * inv;
       float dq_hw, dq_ref;
       const uint32_t c_hw = mx4_encode_hw(w[j], inv, scale, &dq_hw);
@@ -70,17 +88,82 @@ __global__ void check_kernel(int e, unsigned long long* counts) {
     if (loc[k]) atomicAdd(&counts[k], static_cast<unsigned long long>(loc[k]));
 }
 
+// one d significand per thread, every a significand
+__global__ void div_pairs_kernel(uint32_t d0, uint32_t stride, unsigned long long* counts) {
+  const uint32_t id = d0 + (blockIdx.x * blockDim.x + threadIdx.x) * stride;
+  if (id >= (1u << 23)) return;
+  const float d = u2f(0x3f800000u | id);
+  const float y = div_exact_recip(d);
+  unsigned n = 0;
+  for (uint32_t ia = 0; ia < (1u << 23); ++ia) {
+    const float a = u2f(0x3f800000u | ia);
+    n += f2u(div_exact(a, d, y)) != f2u(a / d);
+  }
+  if (n) atomicAdd(&counts[0], static_cast<unsigned long long>(n));
+}
+
+__device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// blockIdx.x = exponent pair, 256 threads x 16 samples each
+__global__ void div_ranges_kernel(unsigned long long* counts) {
+  const int ea = static_cast<int>(blockIdx.x % 258) - 130;
+  const int ed = static_cast<int>(blockIdx.x / 258) - 30;
+  unsigned n = 0;
+  for (int s = 0; s < 16; ++s) {
+    const uint32_t h = mix32(blockIdx.x * 4096u + threadIdx.x * 16u + s);
+    const uint32_t h2 = mix32(h ^ 0x9e3779b9u);
+    float a = u2f(0x3f800000u | (h & 0x7fffffu)) * exp2_int(ea < -127 ? -127 : ea);
+    if (ea < -127) a = a * exp2_int(ea + 127);  // subnormal (or zero) a
+    if (s == 0 && threadIdx.x == 0) a = 0.0f;
+    if (h & 0x80000000u) a = -a;
+    const float d = u2f(0x3f800000u | (h2 & 0x7fffffu)) * exp2_int(ed);
+    n += f2u(div_exact(a, d, div_exact_recip(d))) != f2u(a / d);
+  }
+  if (n) atomicAdd(&counts[1], static_cast<unsigned long long>(n));
+}
+
 }  // namespace
 
-// Runs the check for scale exponent e in [-127, 127]; counts: host array of 8.
+// Runs the MX check for scale exponent e in [-127, 127]; counts: host array of 8.
 extern "C" int mgq_hwcheck_mx(int e, unsigned long long* counts) {
   if (e < -127 || e > 127) return -1;
   unsigned long long* d = nullptr;
   if (hipMalloc(&d, kKinds * sizeof(unsigned long long)) != hipSuccess) return -2;
   hipMemset(d, 0, kKinds * sizeof(unsigned long long));
-  check_kernel<<<(1u << 24) / 256, 256>>>(e, d);
+  check_kernel<<<(1u << 22) / 256, 256>>>(e, d);
   hipError_t err = hipDeviceSynchronize();
   if (err == hipSuccess) err = hipMemcpy(counts, d, kKinds * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  hipFree(d);
+  return err == hipSuccess ? 0 : -3;
+}
+
+// Runs the division check; counts: host array of 2.
+extern "C" int mgq_hwcheck_div(int stride_log, unsigned long long* counts) {
+  if (stride_log < 0 || stride_log > 23) return -1;
+  unsigned long long* d = nullptr;
+  if (hipMalloc(&d, 2 * sizeof(unsigned long long)) != hipSuccess) return -2;
+  hipMemset(d, 0, 2 * sizeof(unsigned long long));
+  const uint32_t stride = 1u << stride_log;
+  const uint32_t n_d = (1u << 23) >> stride_log;  // d significands checked
+  const uint32_t per = 1u << 18;                  // per launch
+  hipError_t err = hipSuccess;
+  for (uint32_t k = 0; k < n_d && err == hipSuccess; k += per) {
+    const uint32_t cnt = n_d - k < per ? n_d - k : per;
+    div_pairs_kernel<<<(cnt + 255) / 256, 256>>>(k * stride, stride, d);
+    err = hipDeviceSynchronize();
+  }
+  if (err == hipSuccess) {
+    div_ranges_kernel<<<258 * 61, 256>>>(d);
+    err = hipDeviceSynchronize();
+  }
+  if (err == hipSuccess) err = hipMemcpy(counts, d, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
   hipFree(d);
   return err == hipSuccess ? 0 : -3;
 }

@@ -42,3 +42,21 @@ def test_hw_mx_conversions_exhaustive(e):
     assert lib.mgq_hwcheck_mx(e, counts) == 0
     bad = {k: int(c) for k, c in zip(KINDS, counts) if c}
     assert not bad, (e, bad)
+
+
+def test_markstein_division_matches_ieee():
+    """div_exact (the recurrence's err = (w - dq) / U[c,c], gptq.py:160-170)
+    against IEEE fp32 division, bit for bit: every 64th divisor significand
+    against all 2^23 dividend significands (the full 2^46 pairs were checked
+    the same way with stride 1), plus random pairs over the exponent range
+    on both sides of the guards."""
+    import torch
+
+    assert torch.cuda.is_available()
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} missing: run build() first")
+    lib = ctypes.CDLL(LIB)
+    lib.mgq_hwcheck_div.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_ulonglong)]
+    counts = (ctypes.c_ulonglong * 2)()
+    assert lib.mgq_hwcheck_div(6, counts) == 0
+    assert list(counts) == [0, 0]
