@@ -212,6 +212,23 @@ int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, f
                   float* rel_err, int32_t* attempts, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* The two halves of mgq_gptq_mxfp, for a caller that wants the attempts
+ * before the solve finishes. The reference computes _prepare_hinv
+ * (gptq.py:27-66, after the dead-column fix of gptq.py:216-222) to
+ * completion -- warnings and RuntimeError included -- before its group loop
+ * (gptq.py:99-180); reading `attempts` after mgq_gptq_mxfp_prepare and before
+ * the solve's outputs gives that order without waiting for the solve.
+ * prepare: the dead-column fix (H in place) and the per-group damped
+ * Cholesky-inverse into `workspace`, attempts as in mgq_gptq_mxfp.
+ * solve: the fused group solver on a workspace prepared for the same
+ * B, R, C (the same argument meanings as mgq_gptq_mxfp). */
+int mgq_gptq_mxfp_prepare(float* H, int64_t B, int64_t R, int64_t C, float damp, int max_attempts,
+                          int32_t* attempts, void* workspace, int64_t workspace_bytes, void* stream);
+int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, int mode,
+                        int algorithm, const int32_t* offsets, int n_offsets, uint8_t* q_out,
+                        uint8_t* scales_out, float* W_dq, float* rel_err, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes needed by mgq_hinv_full_pass for H [B, C, C] (two fp64
  * [B, C, C] arrays). */
 int64_t mgq_hinv_full_workspace_size(int64_t B, int64_t C);

@@ -620,12 +620,36 @@ extern "C" int64_t mgq_gptq_mxfp_workspace_size(int64_t B, int64_t R, int64_t C)
   return ws_layout(B, R, C).total;
 }
 
-extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
-                             float* H, int mode, int algorithm, float damp, int max_attempts,
-                             const int32_t* offsets, int n_offsets, uint8_t* q_out,
-                             uint8_t* scales_out, float* W_dq, float* rel_err,
-                             int32_t* attempts, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
+extern "C" int mgq_gptq_mxfp_prepare(float* H, int64_t B, int64_t R, int64_t C, float damp,
+                                     int max_attempts, int32_t* attempts, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  clear_error();
+  MGQ_REQUIRE(B >= 0 && R >= 0 && C >= 0, MGQ_ERR_SHAPE, "bad shape");
+  MGQ_REQUIRE(C % kG == 0, MGQ_ERR_SHAPE, "in_features %lld not divisible by group %d",
+              (long long)C, kG);
+  MGQ_REQUIRE(max_attempts >= 1, MGQ_ERR_VALUE, "max_attempts must be >= 1");
+  const WsLayout L = ws_layout(B, R, C);
+  MGQ_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MGQ_ERR_WORKSPACE,
+              "mxfp workspace %lld < %lld bytes", (long long)workspace_bytes,
+              (long long)L.total);
+  MGQ_REQUIRE((reinterpret_cast<uintptr_t>(H) & 15u) == 0, MGQ_ERR_SHAPE,
+              "H must be 16-byte aligned");
+  if (B == 0 || C == 0) return MGQ_OK;
+  hipStream_t st = as_stream(stream);
+  char* ws = static_cast<char*>(workspace);
+  uint8_t* dead = reinterpret_cast<uint8_t*>(ws + L.dead_off);
+  float* U = reinterpret_cast<float*>(ws + L.u_off);
+  float* Hcmp = reinterpret_cast<float*>(ws + L.hc_off);
+  dead_fix_kernel<<<elementwise_blocks(B * C, 256), 256, 0, st>>>(H, B, C, dead);
+  if (int rc = check_launch("dead-column fix")) return rc;
+  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st);
+}
+
+extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
+                                   int mode, int algorithm, const int32_t* offsets, int n_offsets,
+                                   uint8_t* q_out, uint8_t* scales_out, float* W_dq,
+                                   float* rel_err, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
   clear_error();
   MGQ_REQUIRE(mode == kMxfp4 || mode == kMxfp8, MGQ_ERR_VALUE, "not a microscaling mode: %d",
               mode);
@@ -636,7 +660,6 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
   MGQ_REQUIRE(B >= 0 && R >= 0 && C >= 0, MGQ_ERR_SHAPE, "bad shape");
   MGQ_REQUIRE(C % kG == 0, MGQ_ERR_SHAPE, "in_features %lld not divisible by group %d",
               (long long)C, kG);
-  MGQ_REQUIRE(max_attempts >= 1, MGQ_ERR_VALUE, "max_attempts must be >= 1");
   Offsets offs{0, {0}};
   if (algorithm == 1) {
     MGQ_REQUIRE(offsets != nullptr && n_offsets >= 1 && n_offsets <= kMaxOffsets, MGQ_ERR_VALUE,
@@ -651,22 +674,16 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
   MGQ_REQUIRE(rel_err == nullptr || static_cast<const void*>(W_dq) != W, MGQ_ERR_VALUE,
               "rel_err needs W_dq separate from W (in-place solves skip rel_err)");
   MGQ_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
-                  (reinterpret_cast<uintptr_t>(H) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(W_dq) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0,
-              MGQ_ERR_SHAPE, "W, H, W_dq and q_out must be 16-byte aligned");
-  if (B == 0 || C == 0) return MGQ_OK;
+              MGQ_ERR_SHAPE, "W, W_dq and q_out must be 16-byte aligned");
+  if (B == 0 || C == 0 || R == 0) return MGQ_OK;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
-  uint8_t* dead = reinterpret_cast<uint8_t*>(ws + L.dead_off);
-  float* U = reinterpret_cast<float*>(ws + L.u_off);
-  float* Hcmp = reinterpret_cast<float*>(ws + L.hc_off);
+  const uint8_t* dead = reinterpret_cast<const uint8_t*>(ws + L.dead_off);
+  const float* U = reinterpret_cast<const float*>(ws + L.u_off);
+  const float* Hcmp = reinterpret_cast<const float*>(ws + L.hc_off);
   double* rel_part = reinterpret_cast<double*>(ws + L.rel_off);
-
-  dead_fix_kernel<<<elementwise_blocks(B * C, 256), 256, 0, st>>>(H, B, C, dead);
-  if (int rc = check_launch("dead-column fix")) return rc;
-  if (int rc = launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st)) return rc;
-  if (R == 0) return MGQ_OK;
   // Candidate errors are exact in bf16 for bf16 weights while every
   // |w / scale| stays below 512 (MXFP4) or 16384 (MXFP8): with e0 the
   // groupwise exponent, |w / 2^(e0+off)| <= fmax * 2^(0.5 - off), so offsets
@@ -695,4 +712,33 @@ extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, i
     if (int rc2 = check_launch("rel_err")) return rc2;
   }
   return MGQ_OK;
+}
+
+extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
+                             float* H, int mode, int algorithm, float damp, int max_attempts,
+                             const int32_t* offsets, int n_offsets, uint8_t* q_out,
+                             uint8_t* scales_out, float* W_dq, float* rel_err,
+                             int32_t* attempts, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  clear_error();
+  // argument checks of both halves before anything is launched
+  MGQ_REQUIRE(mode == kMxfp4 || mode == kMxfp8, MGQ_ERR_VALUE, "not a microscaling mode: %d",
+              mode);
+  MGQ_REQUIRE(algorithm == 0 || algorithm == 1, MGQ_ERR_VALUE,
+              "unsupported MXFP GPTQ algorithm code: %d", algorithm);
+  MGQ_REQUIRE(w_dtype == kF32 || w_dtype == kBF16 || w_dtype == kF16, MGQ_ERR_VALUE,
+              "unsupported weight dtype code %d", w_dtype);
+  MGQ_REQUIRE(algorithm == 0 || (offsets != nullptr && n_offsets >= 1 && n_offsets <= kMaxOffsets),
+              MGQ_ERR_VALUE, "safe-scale-search needs 1..%d exponent offsets", kMaxOffsets);
+  MGQ_REQUIRE(rel_err == nullptr || static_cast<const void*>(W_dq) != W, MGQ_ERR_VALUE,
+              "rel_err needs W_dq separate from W (in-place solves skip rel_err)");
+  MGQ_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(W_dq) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0,
+              MGQ_ERR_SHAPE, "W, W_dq and q_out must be 16-byte aligned");
+  if (int rc = mgq_gptq_mxfp_prepare(H, B, R, C, damp, max_attempts, attempts, workspace,
+                                     workspace_bytes, stream))
+    return rc;
+  return mgq_gptq_mxfp_solve(W, w_dtype, B, R, C, mode, algorithm, offsets, n_offsets, q_out,
+                             scales_out, W_dq, rel_err, workspace, workspace_bytes, stream);
 }

@@ -6,6 +6,7 @@
 
 #include "mgq_capi.h"
 #include "mgq_common.h"
+#include "mx_hw.h"
 
 namespace mgq {
 namespace {
@@ -118,6 +119,63 @@ __global__ void rtn_mxfp_kernel(const void* __restrict__ W, int dtype, int64_t n
       q[g * kMxGroup + i] = static_cast<uint8_t>(mx_quant(v[i], s, mode, &d));
       dq[g * kMxGroup + i] = d;
     }
+  }
+}
+
+// The same for 16-byte aligned W, q and dq: one thread per group with
+// 16-byte loads and stores, and the hardware MX encoders (mx_hw.h, equal to
+// mx_quant for every input: w / s == w * (1/s) for power-of-two s).
+template <typename TIn, bool IS_F16>
+__global__ void rtn_mxfp_vec_kernel(const TIn* __restrict__ W, int64_t n_groups, int mode,
+                                    uint8_t* __restrict__ q, uint8_t* __restrict__ bytes,
+                                    float* __restrict__ dq) {
+  const float fmax = (mode == kMxfp4) ? 6.0f : 448.0f;
+  for (int64_t g = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; g < n_groups;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    float v[kMxGroup];
+    if constexpr (sizeof(TIn) == 4) {
+      const float4* p = reinterpret_cast<const float4*>(W + g * kMxGroup);
+#pragma unroll
+      for (int i = 0; i < kMxGroup / 4; ++i) {
+        const float4 x = p[i];
+        v[4 * i] = x.x, v[4 * i + 1] = x.y, v[4 * i + 2] = x.z, v[4 * i + 3] = x.w;
+      }
+    } else {
+      const uint4* p = reinterpret_cast<const uint4*>(W + g * kMxGroup);
+#pragma unroll
+      for (int i = 0; i < kMxGroup / 8; ++i) {
+        const uint4 x = p[i];
+        const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint16_t lo = static_cast<uint16_t>(d[k] & 0xffffu), hi = static_cast<uint16_t>(d[k] >> 16);
+          v[8 * i + 2 * k] = IS_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+          v[8 * i + 2 * k + 1] = IS_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+        }
+      }
+    }
+    float m = fabsf(v[0]);
+#pragma unroll
+    for (int i = 1; i < kMxGroup; ++i) m = nan_max(m, fabsf(v[i]));
+    const int e = e8m0_exponent(m, fmax);
+    const float s = exp2_int(e), inv = exp2_int(-e);
+    bytes[g] = static_cast<uint8_t>(e + 127);
+    uint32_t codes[kMxGroup / 4];
+    float d[kMxGroup];
+#pragma unroll
+    for (int i = 0; i < kMxGroup / 4; ++i) codes[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < kMxGroup; ++i) {
+      const uint32_t c = (mode == kMxfp4) ? mx4_encode_hw(v[i], inv, s, &d[i])
+                                          : mx8_encode_hw(v[i], inv, s, &d[i]);
+      codes[i / 4] |= c << (8 * (i % 4));
+    }
+    uint4* qp = reinterpret_cast<uint4*>(q + g * kMxGroup);
+    qp[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+    qp[1] = make_uint4(codes[4], codes[5], codes[6], codes[7]);
+    float4* op = reinterpret_cast<float4*>(dq + g * kMxGroup);
+#pragma unroll
+    for (int i = 0; i < kMxGroup / 4; ++i) op[i] = make_float4(d[4 * i], d[4 * i + 1], d[4 * i + 2], d[4 * i + 3]);
   }
 }
 
@@ -288,8 +346,21 @@ extern "C" int mgq_rtn_quantize_mxfp(const void* W, int w_dtype, int64_t rows, i
   MGQ_REQUIRE(rows >= 0 && cols >= 0, MGQ_ERR_SHAPE, "bad shape");
   const int64_t n_groups = rows * (cols / kMxGroup);
   if (n_groups == 0) return MGQ_OK;
-  rtn_mxfp_kernel<<<elementwise_blocks(n_groups, kThreads), kThreads, 0, as_stream(stream)>>>(
-      W, w_dtype, n_groups, mode, q, scale_bytes, dq);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(q) |
+                         reinterpret_cast<uintptr_t>(dq)) & 15u) == 0;
+  const unsigned blocks = elementwise_blocks(n_groups, kThreads);
+  hipStream_t st = as_stream(stream);
+  if (!aligned)
+    rtn_mxfp_kernel<<<blocks, kThreads, 0, st>>>(W, w_dtype, n_groups, mode, q, scale_bytes, dq);
+  else if (w_dtype == kF32)
+    rtn_mxfp_vec_kernel<float, false><<<blocks, kThreads, 0, st>>>(
+        static_cast<const float*>(W), n_groups, mode, q, scale_bytes, dq);
+  else if (w_dtype == kBF16)
+    rtn_mxfp_vec_kernel<uint16_t, false><<<blocks, kThreads, 0, st>>>(
+        static_cast<const uint16_t*>(W), n_groups, mode, q, scale_bytes, dq);
+  else
+    rtn_mxfp_vec_kernel<uint16_t, true><<<blocks, kThreads, 0, st>>>(
+        static_cast<const uint16_t*>(W), n_groups, mode, q, scale_bytes, dq);
   return check_launch("rtn_quantize_mxfp");
 }
 

@@ -83,7 +83,15 @@ def _prepare_hinv(H: torch.Tensor, damp: float, max_attempts: int = 6) -> torch.
 
 def _mxfp_solve(W_in: torch.Tensor, H: torch.Tensor, mode: str, damp: float, algorithm: str,
                 W_out: torch.Tensor, want_rel: bool):
-    """Launch the fused MXFP solver; returns (q, scales, rel|None)."""
+    """Launch the fused MXFP solver; returns (q, scales, rel|None).
+
+    The damped Cholesky-inverse runs first (mgq_gptq_mxfp_prepare); its
+    per-block attempt counts are copied to pinned host memory before the
+    group solver is launched, so the reference's warnings and RuntimeError
+    (gptq.py:37-63) come from a short wait for that copy instead of a wait
+    for the whole solve. In place (W_out is W_in) the solver is only launched
+    once the attempts are known, so a failing call leaves W untouched as the
+    reference's does."""
     if algorithm not in ("groupwise", "safe-scale-search"):
         raise ValueError(f"unsupported MXFP GPTQ algorithm: {algorithm}")
     B, R, C = W_in.shape
@@ -96,22 +104,41 @@ def _mxfp_solve(W_in: torch.Tensor, H: torch.Tensor, mode: str, damp: float, alg
     ws = torch.empty(int(lib.mgq_gptq_mxfp_workspace_size(B, R, C)), dtype=torch.uint8, device=dev)
     offs = MXFP4_OFFSETS if mode == "mxfp4" else MXFP8_OFFSETS
     offs_arr = (ctypes.c_int32 * len(offs))(*offs)  # alive until the call returns
-    nat.call(
-        "mgq_gptq_mxfp", W_in.data_ptr(), nat.dtype_code(W_in.dtype), B, R, C, H.data_ptr(),
-        nat.mode_code(mode), 1 if algorithm == "safe-scale-search" else 0, float(damp), 6,
-        ctypes.addressof(offs_arr), len(offs), q.data_ptr(), scales.data_ptr(), W_out.data_ptr(),
-        None if rel is None else rel.data_ptr(), att.data_ptr(), ws.data_ptr(), ws.numel(),
-        nat.stream_of(dev),
-    )
-    att_h = att.cpu().numpy()  # one small D2H copy: escalation warnings / failure
+    stream = nat.stream_of(dev)
+    nat.call("mgq_gptq_mxfp_prepare", H.data_ptr(), B, R, C, float(damp), 6, att.data_ptr(),
+             ws.data_ptr(), ws.numel(), stream)
+
+    def solve():
+        nat.call(
+            "mgq_gptq_mxfp_solve", W_in.data_ptr(), nat.dtype_code(W_in.dtype), B, R, C,
+            nat.mode_code(mode), 1 if algorithm == "safe-scale-search" else 0,
+            ctypes.addressof(offs_arr), len(offs), q.data_ptr(), scales.data_ptr(), W_out.data_ptr(),
+            None if rel is None else rel.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+        )
+
+    if W_out.data_ptr() == W_in.data_ptr():
+        att_h = att.cpu().numpy()
+        _attempts_report(att_h, B, damp, H, dev)
+        solve()
+        return q, scales, rel
+    att_host = torch.empty(att.shape, dtype=torch.int32, pin_memory=True)
+    att_host.copy_(att, non_blocking=True)
+    copied = torch.cuda.Event()
+    copied.record(torch.cuda.current_stream(dev))
+    solve()
+    copied.synchronize()
+    _attempts_report(att_host.numpy(), B, damp, H, dev)
+    return q, scales, rel
+
+
+def _attempts_report(att_h: np.ndarray, B: int, damp: float, H: torch.Tensor, dev) -> None:
+    """Warnings / RuntimeError of every 32-column group's _prepare_hinv call."""
     if att_h.size == 0 or (att_h.min() == 1 and att_h.max() == 1):
-        return q, scales, rel  # every block factored at the first damping: nothing to report
-    G = C // MX_GROUP_SIZE
-    for g in range(G):
+        return  # every block factored at the first damping: nothing to report
+    for g in range(att_h.shape[0]):
         sl = slice(g * MX_GROUP_SIZE, (g + 1) * MX_GROUP_SIZE)
         _escalation_report(att_h[g], B, damp, 6,
                            lambda idx, sl=sl: H[torch.as_tensor(idx, device=dev)][:, sl, sl])
-    return q, scales, rel
 
 
 @torch.no_grad()

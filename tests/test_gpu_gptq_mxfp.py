@@ -227,3 +227,59 @@ def test_gptq_quantize_in_place_semantics():
         gptq.solve_gptq(Wd, Hd, 4, 32, mode="mxfp4", mxfp_algorithm="bogus")
     with pytest.raises(AssertionError):
         gptq.solve_gptq(Wd[:, :, :48], Hd[:, :48, :48].contiguous(), 4, 32, mode="mxfp4")
+
+
+def test_solver_failure_matches_reference_and_in_place_leaves_w(caplog):
+    """A Hessian block that never factors: solve_gptq raises the reference's
+    RuntimeError after its warnings (gptq.py:37-63, via the dead-column fix
+    of gptq.py:216-222 as the reference's solver applies it); the in-place
+    gptq_quantize raises before touching W."""
+    from mlx_gptq import gptq
+
+    W, H, _ = _setup(B=3, R=8, C=64, seed=4)
+    H[1, 37, 35] = H[1, 35, 37] = float("nan")  # group 1 of item 1 never factors
+    B, C = H.shape[0], H.shape[-1]
+    with caplog.at_level(logging.WARNING, logger="oracle.gptq_ref"):
+        with pytest.raises(RuntimeError) as ref_err:
+            gptq_ref.solve_gptq(W.clone(), H.clone(), 4, 32, mode="mxfp4")
+    ref_msgs = [r.getMessage() for r in caplog.records]
+    caplog.clear()
+    with caplog.at_level(logging.WARNING, logger="mlx_gptq.gptq"):
+        with pytest.raises(RuntimeError) as ei:
+            gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), 4, 32, mode="mxfp4")
+    assert str(ei.value) == str(ref_err.value)
+    assert [r.getMessage() for r in caplog.records] == ref_msgs
+    Wd = W.clone().to(DEV)
+    with pytest.raises(RuntimeError):
+        gptq.gptq_quantize(Wd, H.clone().to(DEV), 4, 32, mode="mxfp4")
+    assert torch.equal(Wd.cpu(), W)
+
+
+def test_one_call_entry_point_equals_prepare_then_solve():
+    """mgq_gptq_mxfp (one call) against mgq_gptq_mxfp_prepare +
+    mgq_gptq_mxfp_solve (what solve_gptq uses): identical outputs."""
+    import ctypes
+
+    from mlx_gptq import _native as nat
+    from mlx_gptq import gptq
+
+    W, H, _ = _setup(B=2, R=96, C=128, seed=9, scale=0.05)
+    Wb = W.to(torch.bfloat16).to(DEV)
+    q1, s1, _, wq1, rel1 = gptq.solve_gptq(Wb, H.clone().to(DEV), 4, 32, mode="mxfp4")
+    B, R, C = W.shape
+    Hd = H.clone().to(DEV)
+    q = torch.empty(B, R, C, dtype=torch.uint8, device=DEV)
+    s = torch.empty(B, R, C // 32, dtype=torch.uint8, device=DEV)
+    wq = torch.empty(B, R, C, dtype=torch.float32, device=DEV)
+    rel = torch.empty(B, dtype=torch.float32, device=DEV)
+    att = torch.empty(C // 32, B, dtype=torch.int32, device=DEV)
+    lib = nat.load()
+    ws = torch.empty(int(lib.mgq_gptq_mxfp_workspace_size(B, R, C)), dtype=torch.uint8, device=DEV)
+    offs = (ctypes.c_int32 * 7)(*gptq.MXFP4_OFFSETS)
+    nat.call("mgq_gptq_mxfp", Wb.data_ptr(), nat.dtype_code(Wb.dtype), B, R, C, Hd.data_ptr(),
+             nat.mode_code("mxfp4"), 1, 0.01, 6, ctypes.addressof(offs), 7, q.data_ptr(),
+             s.data_ptr(), wq.data_ptr(), rel.data_ptr(), att.data_ptr(), ws.data_ptr(), ws.numel(),
+             nat.stream_of(torch.device(DEV)))
+    torch.cuda.synchronize()
+    assert torch.equal(q, q1) and torch.equal(s, s1) and torch.equal(wq, wq1)
+    assert torch.equal(rel, rel1) and bool((att == 1).all())

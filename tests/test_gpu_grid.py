@@ -121,14 +121,21 @@ def test_dequantize_mxfp_all_codes(mode):
 
 
 @pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_rtn_quantize_mxfp_bit_exact(mode, dtype):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shift", [0, 1])
+def test_rtn_quantize_mxfp_bit_exact(mode, dtype, shift):
+    """shift = 1 hands the kernel a W that is not 16-byte aligned (the
+    element-wise path); shift = 0 takes the vectorised hardware-encoder path."""
     from mlx_gptq import grid
 
     g = torch.Generator().manual_seed(4)
     W = (torch.randn(3, 40, 256, generator=g) * torch.exp(torch.randn(3, 40, 1, generator=g) * 3)).to(dtype)
     W[0, 0, :32] = 0.0
-    q, sb, b, dq = grid.rtn_quantize_mxfp(W.to(DEV), mode)
+    W[0, 1, :4] = torch.tensor([-0.0, 1e-40, -1e-40, 0.0]).to(dtype)
+    flat = torch.zeros(W.numel() + shift, dtype=dtype, device=DEV)
+    Wd = flat[shift:].view(W.shape)
+    Wd.copy_(W.to(DEV))
+    q, sb, b, dq = grid.rtn_quantize_mxfp(Wd, mode)
     rq, rsb, rb, rdq = grid_ref.rtn_quantize_mxfp(W, mode)
     assert b is None and rb is None
     assert torch.equal(q.cpu(), rq) and torch.equal(sb.cpu(), rsb)
