@@ -33,6 +33,8 @@ namespace {
 constexpr int kNb = 64;  // leaf block
 constexpr int kGT = 64;  // GEMM output tile edge
 
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+
 // lam[b] = fp32(max(mean(diag H_b), 1e-8) * damp[b]): fp64 diagonal sum
 // rounded once, then the reference's fp32 clamp and product.
 __global__ void __launch_bounds__(256)
@@ -76,123 +78,96 @@ __global__ void build_kernel(const float* __restrict__ H, int64_t C, const float
   }
 }
 
-// Leaf: the n x n (n <= 64) diagonal block at r0, 256 threads, the block
-// in registers as 4x4 tiles (thread (tr, tc) owns rows 4tr.., columns
-// 4tc..). Right-looking UL factor from the last column:
-//   V[j][j] = sqrt(M[j][j]),  V[i][j] = M[i][j] / V[j][j]  (i < j),
-//   M[i][k] -= V[i][j] V[k][j]  (i <= k < j),
-// with column j broadcast through LDS; then W = V^-1 by back substitution
-// on X = I:  W[r][:] = X[r][:] / V[r][r],  X[i][:] -= V[i][r] W[r][:] (i < r).
-// Broadcast buffers alternate between steps, so each step needs two
-// barriers. Entries below the diagonal of M are never read. Writes W's
-// block (zeros below the diagonal).
-__global__ void __launch_bounds__(256)
+// Leaf: W = V^-1 for the n x n (n <= 64) diagonal block A_b = V V^T at r0
+// (V upper). One wavefront per batch item, no workgroup barrier: lanes form
+// an 8 x 8 grid (p = lane / 8, q = lane % 8) and lane (p, q) holds rows
+// 8p..8p+7 x columns 8q..8q+7 of the working matrix R in 64 fp64 registers.
+// The sweep over j = 63 .. 0 does the factor step and the Gauss-Jordan step
+// of the inverse at once (the 32 x 32 kernel of cholesky.hip does the same):
+// with a = row j of R (a_k = A[j][k] for k < j, a_j = d the pivot, a_k =
+// unscaled row j of the inverse for k > j) and c_i = a_i / d, every row
+// i < j does R[i][k] -= c_i a_k (k != j) and R[i][j] = -c_i. Row j is final
+// after its step; at the end W[i][k] = R[i][k] / sqrt(d_i) for k > i and
+// W[i][i] = 1 / sqrt(d_i). Each step the 8 lanes holding row j publish it
+// through LDS (512 bytes) and every lane reads the 8 entries of its rows and
+// the 8 of its columns: 64 FMAs per lane-step. Only the lower triangle of
+// the block is read; rows past n are identity padding (their steps change
+// nothing). A pivot <= 0 or NaN flags the item as failed.
+__global__ void __launch_bounds__(64)
     leaf_kernel(const double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t r0, int n,
                 const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
   const int64_t b = blockIdx.x;
   if (!active[b] || failed[b]) return;
-  const int tid = threadIdx.x;
-  const int tr = tid >> 4, tc = tid & 15;
-  __shared__ double piv[2];
-  __shared__ double colv[2][kNb];
-  __shared__ double wrow[2][kNb];
+  __shared__ __attribute__((aligned(16))) double bc[kNb];
+  const int lane = threadIdx.x;
+  const int p = lane >> 3, q = lane & 7;
   const double* Ab = A + b * C * C + r0 * C + r0;
-  double a[4][4];
+  double R[8][8];
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int r = 0; r < 8; ++r) {
+    const int i = 8 * p + r;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = tr * 4 + p, k = tc * 4 + q;
-      a[p][q] = (i < n && k < n) ? Ab[i * C + k] : 0.0;
-    }
-  // columns in groups of 4 so the column inside a tile is a constant (the
-  // register arrays stay in registers)
-  for (int jb = (n - 1) >> 2; jb >= 0; --jb) {
-#pragma unroll
-    for (int jq = 3; jq >= 0; --jq) {
-      const int j = jb * 4 + jq;
-      if (j >= n) continue;  // uniform
-      const int par = j & 1;
-      if (tr == jb && tc == jb) piv[par] = a[jq][jq];
-      __syncthreads();
-      const double d = piv[par];
-      if (!(d > 0.0)) {  // uniform
-        if (tid == 0) failed[b] = 1;
-        return;
-      }
-      const double sd = sqrt(d);
-      const double rs = 1.0 / sd;  // fp64: scaling by the reciprocal is exact to ~1 ulp
-      if (tc == jb) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const int i = tr * 4 + p;
-          const double v = i < j ? a[p][jq] * rs : (i == j ? sd : 0.0);
-          colv[par][i] = v;
-          if (i <= j) a[p][jq] = v;
-        }
-      }
-      __syncthreads();
-      double ci[4], ck[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) ci[p] = colv[par][tr * 4 + p];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) ck[q] = colv[par][tc * 4 + q];
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i = tr * 4 + p, k = tc * 4 + q;
-          if (i <= k && k < j) a[p][q] = a[p][q] - ci[p] * ck[q];
-        }
+    for (int c = 0; c < 8; ++c) {
+      const int k = 8 * q + c;
+      R[r][c] = (i < n && k < n) ? (k <= i ? Ab[i * C + k] : 0.0) : (i == k ? 1.0 : 0.0);
     }
   }
-  // X = I, then back substitution; V's column r comes from a (final).
-  double x[4][4];
+  double piv[8];
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int r = 0; r < 8; ++r) piv[r] = 1.0;
+  bool ok = true;
+#pragma unroll 1
+  for (int jp = 7; jp >= 0; --jp) {
+    const bool own_row = (p == jp), own_col = (q == jp);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) x[p][q] = (tr * 4 + p == tc * 4 + q) ? 1.0 : 0.0;
-  for (int rb = (n - 1) >> 2; rb >= 0; --rb) {
+    for (int jr = 7; jr >= 0; --jr) {
+      const int j = 8 * jp + jr;
+      if (own_row) {  // the 8 lanes holding row j publish it
 #pragma unroll
-    for (int rq = 3; rq >= 0; --rq) {
-      const int r = rb * 4 + rq;
-      if (r >= n) continue;  // uniform
-      const int par = r & 1;
-      if (tc == rb) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) colv[par][tr * 4 + p] = a[p][rq];  // V[i][r]
+        for (int c = 0; c < 8; c += 2)
+          *reinterpret_cast<f64x2_t*>(bc + 8 * q + c) = f64x2_t{R[jr][c], R[jr][c + 1]};
       }
-      __syncthreads();
-      if (tr == rb) {
-        const double ivr = 1.0 / colv[par][r];
+      __builtin_amdgcn_wave_barrier();
+      double ai[8], ak[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) wrow[par][tc * 4 + q] = x[rq][q] * ivr;
+      for (int c = 0; c < 8; c += 2) {
+        const f64x2_t u = *reinterpret_cast<const f64x2_t*>(bc + 8 * p + c);
+        const f64x2_t v = *reinterpret_cast<const f64x2_t*>(bc + 8 * q + c);
+        ai[c] = u.x, ai[c + 1] = u.y, ak[c] = v.x, ak[c + 1] = v.y;
       }
-      __syncthreads();
-      double vi[4], wc[4];
+      const double d = bc[j];
+      __builtin_amdgcn_wave_barrier();
+      ok = ok & (d > 0.0);
+      const double rd = recip_f64(d);
+      piv[jr] = own_row ? d : piv[jr];
+      double cf[8];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) vi[p] = colv[par][tr * 4 + p];
+      for (int r = 0; r < 8; ++r) cf[r] = (8 * p + r < j) ? ai[r] * rd : 0.0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) wc[q] = wrow[par][tc * 4 + q];
+      for (int r = 0; r < 8; ++r) {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int i = tr * 4 + p;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (i < r) x[p][q] = x[p][q] - vi[p] * wc[q];
-          else if (i == r) x[p][q] = wc[q];
-        }
+        for (int c = 0; c < 8; ++c) R[r][c] = fma(-cf[r], ak[c], R[r][c]);
+        // column j of the inverse: X[i][j] = -c_i (cf is 0 for rows i >= j)
+        if (8 * p + r < j) R[r][jr] = own_col ? -cf[r] : R[r][jr];
       }
     }
+  }
+  if (!__builtin_amdgcn_readfirstlane(ok ? 1 : 0)) {  // d is the same in every lane
+    if (lane == 0) failed[b] = 1;
+    return;
   }
   double* Wb = W + b * C * C + r0 * C + r0;
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int r = 0; r < 8; ++r) {
+    const int i = 8 * p + r;
+    if (i >= n) continue;
+    const double rs = 1.0 / sqrt(piv[r]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = tr * 4 + p, k = tc * 4 + q;
-      if (i < n && k < n) Wb[i * C + k] = x[p][q];
+    for (int c = 0; c < 8; ++c) {
+      const int k = 8 * q + c;
+      if (k < n) Wb[i * C + k] = k > i ? R[r][c] * rs : (k == i ? rs : 0.0);
     }
+  }
 }
 
 // C[m][n] = alpha * sum_k A[m][k] opB[k][n] + beta * C[m][n], opB = B or B^T
@@ -358,7 +333,7 @@ int factor_rec(const Ctx& x, int64_t b0, int64_t b1, int depth) {
   const int64_t C = x.C, CC = C * C;
   const int64_t r0 = b0 * kNb, r1 = std::min(b1 * kNb, C);
   if (b1 - b0 == 1) {
-    leaf_kernel<<<static_cast<unsigned>(x.B), 256, 0, x.s>>>(x.A, x.W, C, r0,
+    leaf_kernel<<<static_cast<unsigned>(x.B), 64, 0, x.s>>>(x.A, x.W, C, r0,
                                                             static_cast<int>(r1 - r0), x.active,
                                                             x.failed);
     return check_launch("hinv leaf");

@@ -42,16 +42,6 @@ constexpr int kWaves = 4;  // blocks per workgroup, one wavefront each
 
 typedef double f64x2_t __attribute__((ext_vector_type(2)));
 
-// 1/d for d > 0: v_rcp_f64 refined by two Newton-Raphson steps
-// y <- y + y (1 - d y), each of which squares the relative error.
-__device__ inline double recip_f64(double d) {
-  double y = __builtin_amdgcn_rcp(d);
-  double e = fma(-d, y, 1.0);
-  y = fma(y, e, y);
-  e = fma(-d, y, 1.0);
-  return fma(y, e, y);
-}
-
 __device__ inline double wave_sum_f64(double v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);

@@ -73,6 +73,16 @@ __device__ inline float load_any(const void* base, int64_t i, int dtype) {
   return load_storage(base, i, dtype);
 }
 
+// 1/d for d > 0: v_rcp_f64 refined by two Newton-Raphson steps
+// y <- y + y (1 - d y), each of which squares the relative error.
+__device__ inline double recip_f64(double d) {
+  double y = __builtin_amdgcn_rcp(d);
+  double e = fma(-d, y, 1.0);
+  y = fma(y, e, y);
+  e = fma(-d, y, 1.0);
+  return fma(y, e, y);
+}
+
 // ---------------------------------------------------------------------------
 // E8M0 shared scale (grid.py:61-79).
 // exponent = clamp(round_half_even(fp32(log2(max_abs / fmax))), -127, 127),
