@@ -31,7 +31,6 @@ namespace mgq {
 namespace {
 
 constexpr int kNb = 64;  // leaf block
-constexpr int kGT = 64;  // GEMM output tile edge
 
 typedef double f64x2_t __attribute__((ext_vector_type(2)));
 
@@ -172,28 +171,30 @@ __global__ void __launch_bounds__(64)
 
 // C[m][n] = alpha * sum_k A[m][k] opB[k][n] + beta * C[m][n], opB = B or B^T
 // (B stored [N][K]); row-major with leading dimensions, one matrix per batch
-// item (item strides sA, sB, sC). 64x64 output tiles, 4x4 per thread; K in
-// chunks of 32 staged through LDS, the next chunk's global loads in flight
-// (registers) while the current one is multiplied. UPPER skips tiles
-// strictly below the diagonal.
-constexpr int kGK2 = 32;
+// item (item strides sA, sB, sC). fp64 MFMA (v_mfma_f64_16x16x4f64, whose
+// operand layout is A[l%16][k], B[k][l%16] with k = l/16 per k-step, and
+// result register r of lane l = D[l/16 + 4r][l%16]). A workgroup computes a
+// 32 x 32 output tile as 2 x 2 MFMA blocks; its four waves split K in
+// chunks of 16 (wave w takes chunks w, w+4, ...), each lane loading its four
+// consecutive k of A and opB straight from global memory (the next chunk's
+// loads in flight while the current one is multiplied; lane group l/16 of
+// k-step t takes k = chunk + 4(l/16) + t, the same permutation of k for both
+// operands). The four partial tiles are summed through LDS in wave order, so
+// the result is deterministic. UPPER skips the tiles strictly below the
+// 64-block diagonal (a leaf reads the lower triangle of its 64-block).
+constexpr int kMt = 32;  // output tile edge
+constexpr int kKc = 16;  // k per chunk and wave
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
-template <bool TRANSB>
-__device__ inline void gemm_load(const double* __restrict__ Ab, int64_t lda,
-                                 const double* __restrict__ Bb, int64_t ldb, int M, int N, int K,
-                                 int m0, int n0, int k0, int tid, double (&ra)[8],
-                                 double (&rb)[8]) {
+// v[t] = p[t * stride] for t < cnt (0 past it); 16-byte loads where p allows
+__device__ inline void load4(const double* __restrict__ p, int64_t stride, int cnt, double (&v)[4]) {
+  if (cnt >= 4 && stride == 1 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+    const f64x2_t lo = *reinterpret_cast<const f64x2_t*>(p);
+    const f64x2_t hi = *reinterpret_cast<const f64x2_t*>(p + 2);
+    v[0] = lo.x, v[1] = lo.y, v[2] = hi.x, v[3] = hi.y;
+  } else {
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int e = tid + q * 256;  // 64 x 32 elements
-    const int m = e / kGK2, kk = e % kGK2;
-    ra[q] = (m0 + m < M && k0 + kk < K) ? Ab[(int64_t)(m0 + m) * lda + k0 + kk] : 0.0;
-    if (TRANSB) {
-      rb[q] = (n0 + m < N && k0 + kk < K) ? Bb[(int64_t)(n0 + m) * ldb + k0 + kk] : 0.0;
-    } else {
-      const int kr = e / kGT, nn = e % kGT;
-      rb[q] = (n0 + nn < N && k0 + kr < K) ? Bb[(int64_t)(k0 + kr) * ldb + n0 + nn] : 0.0;
-    }
+    for (int t = 0; t < 4; ++t) v[t] = t < cnt ? p[t * stride] : 0.0;
   }
 }
 
@@ -205,55 +206,84 @@ __global__ void __launch_bounds__(256)
                  const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
   const int64_t item = blockIdx.z;
   if (!active[item] || failed[item]) return;
-  const int m0 = blockIdx.y * kGT, n0 = blockIdx.x * kGT;
-  if (UPPER && n0 + kGT <= m0) return;
+  const int m0 = blockIdx.y * kMt, n0 = blockIdx.x * kMt;
+  if (UPPER && (n0 >> 6) < (m0 >> 6)) return;
   const double* Ab = A + item * sA;
   const double* Bb = B + item * sB;
   double* Cb = Cm + item * sC;
-  __shared__ double As[kGK2][kGT + 1];
-  __shared__ double Bs[kGK2][kGT + 1];
-  const int tid = threadIdx.x;
-  const int tx = tid % 16, ty = tid / 16;
-  double acc[4][4] = {};
-  double ra[8], rb[8];
-  gemm_load<TRANSB>(Ab, lda, Bb, ldb, M, N, K, m0, n0, 0, tid, ra, rb);
-  for (int k0 = 0; k0 < K; k0 += kGK2) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, g = lane >> 4;
+  // this lane's A rows and opB columns; rows / columns past M / N read zeros
+  const double* ap[2];
+  const double* bp[2];
+  bool aok[2], bok[2];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int e = tid + q * 256;
-      As[e % kGK2][e / kGK2] = ra[q];
-      if (TRANSB) {
-        Bs[e % kGK2][e / kGK2] = rb[q];
-      } else {
-        Bs[e / kGT][e % kGT] = rb[q];
+  for (int h = 0; h < 2; ++h) {
+    const int m = m0 + 16 * h + li, n = n0 + 16 * h + li;
+    aok[h] = m < M;
+    bok[h] = n < N;
+    ap[h] = Ab + static_cast<int64_t>(aok[h] ? m : 0) * lda;
+    bp[h] = TRANSB ? Bb + static_cast<int64_t>(bok[h] ? n : 0) * ldb : Bb + (bok[h] ? n : 0);
+  }
+  auto load_chunk = [&](int kc, double (&a)[2][4], double (&b)[2][4]) {
+    const int kb = kc + 4 * g;
+    const int cnt = K - kb < 0 ? 0 : (K - kb > 4 ? 4 : K - kb);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      load4(ap[h] + kb, 1, aok[h] ? cnt : 0, a[h]);
+      if (TRANSB)
+        load4(bp[h] + kb, 1, bok[h] ? cnt : 0, b[h]);
+      else
+        load4(bp[h] + static_cast<int64_t>(kb) * ldb, ldb, bok[h] ? cnt : 0, b[h]);
+    }
+  };
+  f64x4_t acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+  int kc = wave * kKc;
+  if (kc < K) {
+    double a[2][4], b[2][4];
+    load_chunk(kc, a, b);
+    for (; kc < K; kc += 4 * kKc) {
+      double na[2][4], nb[2][4];
+      const bool more = kc + 4 * kKc < K;
+      if (more) load_chunk(kc + 4 * kKc, na, nb);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[x][t], b[y][t], acc[x][y], 0, 0, 0);
+      if (more) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) a[x][t] = na[x][t], b[x][t] = nb[x][t];
       }
     }
-    __syncthreads();
-    if (k0 + kGK2 < K) gemm_load<TRANSB>(Ab, lda, Bb, ldb, M, N, K, m0, n0, k0 + kGK2, tid, ra, rb);
-#pragma unroll 8
-    for (int kk = 0; kk < kGK2; ++kk) {
-      double av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fma(av[i], bv[j], acc[i][j]);
-    }
-    __syncthreads();
   }
+  __shared__ double red[4][4][4][64];  // wave, block (2x+y), register, lane
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + ty * 4 + i;
-    if (m >= M) continue;
+  for (int x = 0; x < 2; ++x)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nn = n0 + tx * 4 + j;
-      if (nn >= N) continue;
-      double* p = Cb + (int64_t)m * ldc + nn;
-      *p = beta == 0.0 ? alpha * acc[i][j] : alpha * acc[i][j] + beta * *p;
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][2 * x + y][r][lane] = acc[x][y][r];
+  __syncthreads();
+  // thread (part = wave, lane) finishes block part: rows l/16 + 4r, column l%16
+  const int x = wave >> 1, y = wave & 1;
+  const int n = n0 + 16 * y + li;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const double v = ((red[0][wave][r][lane] + red[1][wave][r][lane]) + red[2][wave][r][lane]) +
+                     red[3][wave][r][lane];
+    const int m = m0 + 16 * x + g + 4 * r;
+    if (m < M && n < N) {
+      double* p = Cb + static_cast<int64_t>(m) * ldc + n;
+      *p = beta == 0.0 ? alpha * v : alpha * v + beta * *p;
     }
   }
 }
@@ -320,7 +350,7 @@ template <bool TRANSB, bool UPPER = false>
 int gemm(const Ctx& x, const double* A, int64_t lda, int64_t sA, const double* Bm, int64_t ldb,
          int64_t sB, double* Cm, int64_t ldc, int64_t sC, int64_t M, int64_t N, int64_t K,
          double alpha, double beta) {
-  dim3 grid(static_cast<unsigned>(ceil_div(N, kGT)), static_cast<unsigned>(ceil_div(M, kGT)),
+  dim3 grid(static_cast<unsigned>(ceil_div(N, kMt)), static_cast<unsigned>(ceil_div(M, kMt)),
             static_cast<unsigned>(x.B));
   dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(A, lda, sA, Bm, ldb, sB, Cm, ldc, sC,
                                                      static_cast<int>(M), static_cast<int>(N),

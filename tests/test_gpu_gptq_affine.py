@@ -124,11 +124,12 @@ def test_affine_config1_shape_vs_oracle():
     assert torch.allclose(rel.cpu(), rrel, rtol=1e-2)
 
 
-def test_prepare_hinv_full_vs_fp64():
+@pytest.mark.parametrize("C", [320, 200])  # 5 diagonal 64-blocks; 3 and a ragged 8-row block
+def test_prepare_hinv_full_vs_fp64(C):
     from mlx_gptq import gptq
 
     g = torch.Generator().manual_seed(3)
-    B, C = 3, 320  # not a multiple of the 64-wide diagonal blocks
+    B = 3
     A = torch.randn(B, C, 2 * C, generator=g) * torch.exp(torch.randn(B, C, 1, generator=g))
     H = A @ A.transpose(1, 2)
     U = gptq._prepare_hinv(H.to(DEV), 0.01).cpu()
