@@ -17,6 +17,7 @@
 // (the reference's bmm) as an fp32 GEMM.
 #include "mgq_capi.h"
 #include "mgq_common.h"
+#include "mx_hw.h"
 
 namespace mgq {
 namespace {
@@ -24,6 +25,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kMaxBlock = 2048;  // errs of one block per wave in LDS: 32 KB
 constexpr int kMaxShrinks = 128;
+constexpr int kCand = 12;  // clip candidates scored per butterfly
 
 struct Shrinks {
   int n;
@@ -39,19 +41,31 @@ __device__ inline float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
   return v;
 }
-__device__ inline float wave_nan_min(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = nan_min(v, __shfl_xor(v, off));
-  return v;
-}
-__device__ inline float wave_nan_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off));
-  return v;
+
+// a / d for d > 0 (or NaN), correctly rounded: Markstein's correction from
+// y = div_exact_recip(d) (mx_hw.h); a zero numerator is returned as is (a / d
+// keeps its sign for d > 0); outside the correction's range the IEEE
+// division. Every divisor here is positive: the clip scale (range >= 0) and
+// U's diagonal.
+__device__ inline float div_pos(float a, float d, float y) {
+  const float q = a * y;
+  const float r = fmaf(-q, d, a);
+  float e = fmaf(r, y, q);
+  const uint32_t ea = f2u(a) & 0x7f800000u;
+  const bool slow = a != 0.0f && (!(y != 0.0f) || (ea - (27u << 23)) > (200u << 23));
+  // the IEEE division only when some lane needs it: a wave-uniform branch
+  // (the empty asm keeps the compiler from hoisting the division out of it)
+  if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+    asm volatile("" ::: "memory");
+    const float ref = a / d;
+    e = slow ? ref : e;
+  }
+  return a == 0.0f ? a : e;
 }
 
-__device__ inline float affine_q(float w, float b, float s_safe, float maxq) {
-  float q = rintf((w - b) / s_safe);
+// grid.py:215-221: q = clamp(rne((w - b) / s_safe), 0, maxq); ys = RN(1/s_safe)
+__device__ inline float affine_q(float w, float b, float s_safe, float ys, float maxq) {
+  float q = rintf(div_pos(w - b, s_safe, ys));
   if (q != q) return q;
   return fminf(fmaxf(q, 0.0f), maxq);
 }
@@ -77,63 +91,125 @@ __global__ void dead_fix_h_kernel(float* __restrict__ H, int64_t B, int64_t C) {
   }
 }
 
-// Four shrink candidates' error sums reduced together: the same butterfly
-// (and so the same rounding) as wave_sum, with the shuffle latencies of the
-// four chains overlapped.
-__device__ inline void wave_sum4(float (&v)[4]) {
+// N shrink candidates' error sums reduced together: the same butterfly (and
+// so the same rounding) as wave_sum, with the shuffle latencies of the N
+// chains overlapped.
+template <int N>
+__device__ inline void wave_sum_n(float (&v)[N]) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    float t[4];
+    float t[N];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t[i] = __shfl_xor(v[i], off);
+    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], off);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += t[i];
+    for (int i = 0; i < N; ++i) v[i] += t[i];
+  }
+}
+
+// wave_nan_min and wave_nan_max of two values in one butterfly
+__device__ inline void wave_nan_minmax(float& lo, float& hi) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float a = __shfl_xor(lo, off), b = __shfl_xor(hi, off);
+    lo = nan_min(lo, a);
+    hi = nan_max(hi, b);
   }
 }
 
 // Row k of U restricted to the group's columns: lane t holds U[k][j + t + 64 s].
-template <int CPL>
-__device__ inline void load_urow(const float* __restrict__ Ub, int64_t C, int64_t k, int64_t j,
-                                 int lane, const bool (&act)[CPL], float (&u)[CPL]) {
-  const float* Uk = Ub + k * C + j;
+// LDSU: from the block's copy Ublk[(k - i1) * n + (col - i1)] in LDS, else
+// from global memory.
+template <int CPL, bool LDSU>
+__device__ inline void load_urow(const float* __restrict__ Ub, const float* Ublk, int64_t C,
+                                 int64_t i1, int n, int64_t k, int64_t j, int lane,
+                                 const bool (&act)[CPL], float (&u)[CPL]) {
+  if constexpr (LDSU) {
+    const float* Uk = Ublk + (k - i1) * n + (j - i1);
 #pragma unroll
-  for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
+    for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
+  } else {
+    const float* Uk = Ub + k * C + j;
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
+  }
 }
 
-template <int CPL>
+// Grid (ceil(R / 4), B): the four waves of a workgroup take rows of one
+// batch item. LDSU (blocks of at most kLdsBlock columns): the workgroup first
+// copies the block's U[i1:i1+n, i1:i1+n] to LDS, so the column loop and the
+// in-block updates read U rows from LDS instead of all waves fetching the
+// same row from L2 at once.
+constexpr int kLdsBlock = 128;
+
+template <int CPL, bool LDSU>
 __global__ void __launch_bounds__(kWaves * 64)
     affine_block_kernel(float* __restrict__ W, const float* __restrict__ U, int64_t B, int64_t R,
                         int64_t C, int64_t i1, int n, int G, float maxq, int storage, Shrinks sh,
                         uint8_t* __restrict__ q_out, void* s_store, void* b_store,
                         float* __restrict__ Err) {
-  extern __shared__ float errs_lds[];  // [kWaves][n]
+  extern __shared__ float smem[];  // errs [kWaves][n], then (LDSU) Ublk [n][n]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* errs = errs_lds + wave * n;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;  // b*R + r
-  if (row >= B * R) return;  // whole wave exits together (no block barriers below)
-  const int64_t b = row / R;
+  float* errs = smem + wave * n;
+  float* Ublk = smem + kWaves * n;
+  const int64_t b = blockIdx.y;
   const float* Ub = U + b * C * C;
+  if constexpr (LDSU) {
+    if ((n & 1) == 0 && (C & 1) == 0 && (i1 & 1) == 0) {
+      // wave w copies rows w, w+4, ...: one 8-byte chunk per lane and row,
+      // sixteen rows' loads in flight before their LDS stores
+      const int half_n = n >> 1;
+      const bool on = lane < half_n;
+      for (int r0 = wave; r0 < n; r0 += kWaves * 16) {
+        float2 v[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const int r = r0 + kWaves * t;
+          v[t] = (on && r < n) ? *reinterpret_cast<const float2*>(Ub + (i1 + r) * C + i1 + 2 * lane)
+                               : float2{0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const int r = r0 + kWaves * t;
+          if (on && r < n) *reinterpret_cast<float2*>(Ublk + r * n + 2 * lane) = v[t];
+        }
+      }
+    } else {
+      for (int e = threadIdx.x; e < n * n; e += kWaves * 64) {
+        const int r = e / n, c = e % n;
+        Ublk[e] = Ub[(i1 + r) * C + i1 + c];
+      }
+    }
+    __syncthreads();
+  }
+  const int64_t r_in = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+  if (r_in >= R) return;  // whole wave exits together (no block barriers below)
+  const int64_t row = b * R + r_in;
   float* Wr = W + row * C;
   const int64_t ng = C / G;
+  // the clip candidates' p / maxq and p, one per lane (batches of 64)
+  const int n_batches = (sh.n + 63) / 64;
   for (int64_t j = i1; j < i1 + n; j += G) {
-    float acc[CPL];
+    float acc[CPL], dg[CPL], yd[CPL];
     bool act[CPL];
 #pragma unroll
     for (int s = 0; s < CPL; ++s) {
       const int col = lane + 64 * s;
       act[s] = col < G;
       acc[s] = act[s] ? Wr[j + col] : 0.0f;
+      // U's diagonal of the lane's column and its reciprocal for div_pos
+      dg[s] = act[s] ? Ub[(j + col) * C + j + col] : 1.0f;
+      yd[s] = div_exact_recip(dg[s]);
     }
-    // earlier in-block updates, in column order; eight rows of U in flight
+    // earlier in-block updates, in column order; sixteen rows of U in flight
     {
       const int64_t kn = j - i1;  // a multiple of G
       int64_t k = 0;
-      for (; k + 8 <= kn; k += 8) {
-        float u[8][CPL];
+      for (; k + 16 <= kn; k += 16) {
+        float u[16][CPL];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) load_urow<CPL>(Ub, C, i1 + k + t, j, lane, act, u[t]);
+        for (int t = 0; t < 16; ++t) load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, i1 + k + t, j, lane, act, u[t]);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < 16; ++t) {
           const float e = errs[k + t];
 #pragma unroll
           for (int s = 0; s < CPL; ++s)
@@ -142,7 +218,7 @@ __global__ void __launch_bounds__(kWaves * 64)
       }
       for (; k < kn; ++k) {
         float u[CPL];
-        load_urow<CPL>(Ub, C, i1 + k, j, lane, act, u);
+        load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, i1 + k, j, lane, act, u);
         const float e = errs[k];
 #pragma unroll
         for (int s = 0; s < CPL; ++s)
@@ -158,33 +234,46 @@ __global__ void __launch_bounds__(kWaves * 64)
         lo = nan_min(lo, acc[s]);
         hi = nan_max(hi, acc[s]);
       }
-    const float wmin = wave_nan_min(lo), wmax = wave_nan_max(hi);
+    wave_nan_minmax(lo, hi);
+    const float wmin = lo, wmax = hi;
     const float range = wmax - wmin;
     float best_err = 0.0f, s32 = 0.0f, b32 = 0.0f;
-    // candidates four at a time (the host pads the list to a multiple of 4
-    // with copies of the last one, which never win a strict '<')
-    for (int c0 = 0; c0 < sh.n; c0 += 4) {
-      float sc[4], bi[4], part[4];
+    for (int bt = 0; bt < n_batches; ++bt) {
+      // lane l prepares candidate 64 bt + l: scale, bias, divisor reciprocal
+      const int cl = 64 * bt + lane < sh.n ? 64 * bt + lane : sh.n - 1;
+      const float sc_l = round_to_storage(range * sh.p_over_maxq[cl], storage);
+      const float bi_l = round_to_storage(wmin * sh.p[cl], storage);
+      const float ss_l = (fabsf(sc_l) < 1e-12f) ? 1.0f : sc_l;
+      const float ys_l = div_exact_recip(ss_l);
+      // candidates kCand at a time, their error sums reduced in one
+      // butterfly; slots past the batch score a copy of its last candidate
+      // (an equal error never replaces the earlier best under strict '<')
+      const int nb = sh.n - 64 * bt < 64 ? sh.n - 64 * bt : 64;
+      for (int c0 = 0; c0 < nb; c0 += kCand) {
+        float sc[kCand], bi[kCand], part[kCand];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = round_to_storage(range * sh.p_over_maxq[c0 + i], storage);
-        bi[i] = round_to_storage(wmin * sh.p[c0 + i], storage);
-        const float ss = (fabsf(sc[i]) < 1e-12f) ? 1.0f : sc[i];
-        part[i] = 0.0f;
+        for (int i = 0; i < kCand; ++i) {
+          const int ci = c0 + i < nb ? c0 + i : nb - 1;
+          sc[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_l), ci));
+          bi[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bi_l), ci));
+          const float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss_l), ci));
+          const float ys = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ys_l), ci));
+          part[i] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < CPL; ++s)
-          if (act[s]) {
-            const float d = affine_q(acc[s], bi[i], ss, maxq) * sc[i] + bi[i] - acc[s];
-            part[i] += d * d;
+          for (int s = 0; s < CPL; ++s)
+            if (act[s]) {
+              const float d = affine_q(acc[s], bi[i], ss, ys, maxq) * sc[i] + bi[i] - acc[s];
+              part[i] += d * d;
+            }
+        }
+        wave_sum_n<kCand>(part);
+#pragma unroll
+        for (int i = 0; i < kCand; ++i) {
+          if ((bt == 0 && c0 + i == 0) || part[i] < best_err) {
+            best_err = part[i];
+            s32 = sc[i];
+            b32 = bi[i];
           }
-      }
-      wave_sum4(part);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (c0 + i == 0 || part[i] < best_err) {
-          best_err = part[i];
-          s32 = sc[i];
-          b32 = bi[i];
         }
       }
     }
@@ -194,55 +283,70 @@ __global__ void __launch_bounds__(kWaves * 64)
       store_storage(b_store, gi, b32, storage);
     }
     const float s_safe = (fabsf(s32) < 1e-12f) ? 1.0f : s32;
-    // Sequential columns of the group. The column's value and U's diagonal
-    // are read from their owner lane (v_readlane, so every lane computes the
-    // same error); U rows arrive four columns ahead.
+    const float ysafe = div_exact_recip(s_safe);
+    // Sequential columns of the group. The column's value, U's diagonal and
+    // its reciprocal are read from the owner lane (v_readlane, so every lane
+    // computes the same error); the owner lane keeps its code, dequantized
+    // value and error for the group's coalesced stores; U rows arrive eight
+    // columns ahead.
+    float qv[CPL], dqv[CPL], ev[CPL];
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) qv[s] = dqv[s] = ev[s] = 0.0f;
     auto column = [&](int c, const float (&uc)[CPL]) __attribute__((always_inline)) {
       const int owner = c & 63, slot = c >> 6;
-      float mine_v = acc[0], diag_v = uc[0];
+      float mine_v = acc[0], diag_v = dg[0], yd_v = yd[0];
 #pragma unroll
       for (int s = 1; s < CPL; ++s)
         if (s == slot) {
           mine_v = acc[s];
-          diag_v = uc[s];
+          diag_v = dg[s];
+          yd_v = yd[s];
         }
       const float mine = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine_v), owner));
       const float diag = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, diag_v), owner));
-      const float q = affine_q(mine, b32, s_safe, maxq);
+      const float ydg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, yd_v), owner));
+      const float q = affine_q(mine, b32, s_safe, ysafe, maxq);
       const float dq = q * s32 + b32;
-      const float e = (mine - dq) / diag;
-      if (lane == owner) {
-        q_out[row * C + j + c] = (q == q) ? static_cast<uint8_t>(q) : 0;
-        Wr[j + c] = dq;
-        errs[j + c - i1] = e;
-        Err[row * n + (j + c - i1)] = e;
-      }
+      const float e = div_pos(mine - dq, diag, ydg);
 #pragma unroll
       for (int s = 0; s < CPL; ++s) {
         const int col = lane + 64 * s;
-        if (act[s] && col > c) acc[s] = acc[s] - e * uc[s];
+        const bool own = col == c;
+        qv[s] = own ? q : qv[s];
+        dqv[s] = own ? dq : dqv[s];
+        ev[s] = own ? e : ev[s];
+        acc[s] = (act[s] && col > c) ? acc[s] - e * uc[s] : acc[s];
       }
     };
-    const int G4 = G & ~3;
-    float ring[4][CPL];
+    const int G8 = G & ~7;
+    float ring[8][CPL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (u < G4) load_urow<CPL>(Ub, C, j + u, j, lane, act, ring[u]);
-    for (int c0 = 0; c0 < G4; c0 += 4) {
+    for (int u = 0; u < 8; ++u)
+      if (u < G8) load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + u, j, lane, act, ring[u]);
+    for (int c0 = 0; c0 < G8; c0 += 8) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const int c = c0 + u;
         float uc[CPL];
 #pragma unroll
         for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
-        if (c + 4 < G4) load_urow<CPL>(Ub, C, j + c + 4, j, lane, act, ring[u]);
+        if (c + 8 < G8) load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c + 8, j, lane, act, ring[u]);
         column(c, uc);
       }
     }
-    for (int c = G4; c < G; ++c) {
+    for (int c = G8; c < G; ++c) {
       float uc[CPL];
-      load_urow<CPL>(Ub, C, j + c, j, lane, act, uc);
+      load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c, j, lane, act, uc);
       column(c, uc);
+    }
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) {
+      if (!act[s]) continue;
+      const int col = lane + 64 * s;
+      q_out[row * C + j + col] = (qv[s] == qv[s]) ? static_cast<uint8_t>(qv[s]) : 0;
+      Wr[j + col] = dqv[s];
+      errs[j + col - i1] = ev[s];
+      Err[row * n + (j + col - i1)] = ev[s];
     }
     // errs[] is read by every lane of this wave at the next group start
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -375,18 +479,21 @@ extern "C" int mgq_gptq_affine_block(float* W, const float* U, int64_t B, int64_
   if (int rc = make_shrinks(bits, method, grid_steps, max_shrink, &sh)) return rc;
   if (B * R == 0) return MGQ_OK;
   hipStream_t s = as_stream(stream);
-  const unsigned blocks = static_cast<unsigned>(ceil_div(B * R, kWaves));
+  const dim3 blocks(static_cast<unsigned>(ceil_div(R, kWaves)), static_cast<unsigned>(B));
   const float maxq = static_cast<float>((1 << bits) - 1);
-  const size_t lds = sizeof(float) * kWaves * static_cast<size_t>(n);
+  const bool ldsu = n <= kLdsBlock;
+  const size_t lds = sizeof(float) * (kWaves * static_cast<size_t>(n) +
+                                      (ldsu ? static_cast<size_t>(n) * n : 0));
+#define AFFINE_LAUNCH(CPL_, LDSU_)                                                          \
+  affine_block_kernel<CPL_, LDSU_><<<blocks, kWaves * 64, lds, s>>>(                        \
+      W, U, B, R, C, i1, static_cast<int>(n), group_size, maxq, storage_dtype, sh, q_out,  \
+      s_store, b_store, Err)
   if (group_size <= 64) {
-    affine_block_kernel<1><<<blocks, kWaves * 64, lds, s>>>(W, U, B, R, C, i1, static_cast<int>(n),
-                                                          group_size, maxq, storage_dtype, sh,
-                                                          q_out, s_store, b_store, Err);
+    if (ldsu) AFFINE_LAUNCH(1, true); else AFFINE_LAUNCH(1, false);
   } else {
-    affine_block_kernel<2><<<blocks, kWaves * 64, lds, s>>>(W, U, B, R, C, i1, static_cast<int>(n),
-                                                          group_size, maxq, storage_dtype, sh,
-                                                          q_out, s_store, b_store, Err);
+    if (ldsu) AFFINE_LAUNCH(2, true); else AFFINE_LAUNCH(2, false);
   }
+#undef AFFINE_LAUNCH
   if (int rc = check_launch("affine block")) return rc;
   if (i1 + n < C) {
     dim3 grid(static_cast<unsigned>(ceil_div(C - i1 - n, kTn)),
