@@ -78,36 +78,38 @@ __global__ void build_kernel(const float* __restrict__ H, int64_t C, const float
 }
 
 // Leaf: W = V^-1 for the n x n (n <= 64) diagonal block A_b = V V^T at r0
-// (V upper). One wavefront per batch item, no workgroup barrier: lanes form
-// an 8 x 8 grid (p = lane / 8, q = lane % 8) and lane (p, q) holds rows
-// 8p..8p+7 x columns 8q..8q+7 of the working matrix R in 64 fp64 registers.
-// The sweep over j = 63 .. 0 does the factor step and the Gauss-Jordan step
-// of the inverse at once (the 32 x 32 kernel of cholesky.hip does the same):
-// with a = row j of R (a_k = A[j][k] for k < j, a_j = d the pivot, a_k =
+// (V upper). One workgroup of four waves per batch item. The sweep over
+// j = 63 .. 0 does the factor step and the Gauss-Jordan step of the inverse
+// at once (the 32 x 32 kernel of cholesky.hip does the same): with a = row j
+// of the working matrix R (a_k = A[j][k] for k < j, a_j = d the pivot, a_k =
 // unscaled row j of the inverse for k > j) and c_i = a_i / d, every row
 // i < j does R[i][k] -= c_i a_k (k != j) and R[i][j] = -c_i. Row j is final
 // after its step; at the end W[i][k] = R[i][k] / sqrt(d_i) for k > i and
-// W[i][i] = 1 / sqrt(d_i). Each step the 8 lanes holding row j publish it
-// through LDS (512 bytes) and every lane reads the 8 entries of its rows and
-// the 8 of its columns: 64 FMAs per lane-step. Only the lower triangle of
-// the block is read; rows past n are identity padding (their steps change
-// nothing). A pivot <= 0 or NaN flags the item as failed.
-__global__ void __launch_bounds__(64)
+// W[i][i] = 1 / sqrt(d_i). Wave w holds columns 16w..16w+15, its lanes an
+// 8 x 8 grid (p = lane / 8, q = lane % 8): lane (p, q) holds rows 8p..8p+7 x
+// columns 16w + 2q, 16w + 2q + 1 (16 fp64 registers). Each step the lanes
+// holding row j publish it through LDS (two alternating buffers, so one
+// workgroup barrier per step) and every lane reads the 8 entries of its
+// rows, its 2 columns and the pivot: 16 FMAs per lane-step. Only the lower
+// triangle of the block is read; rows past n are identity padding. A pivot
+// <= 0 or NaN flags the item as failed.
+__global__ void __launch_bounds__(256)
     leaf_kernel(const double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t r0, int n,
                 const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
   const int64_t b = blockIdx.x;
-  if (!active[b] || failed[b]) return;
-  __shared__ __attribute__((aligned(16))) double bc[kNb];
-  const int lane = threadIdx.x;
+  if (!active[b] || failed[b]) return;  // uniform over the workgroup
+  __shared__ __attribute__((aligned(16))) double bc[2][kNb];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int p = lane >> 3, q = lane & 7;
+  const int k0 = 16 * wave + 2 * q;  // this lane's two columns
   const double* Ab = A + b * C * C + r0 * C + r0;
-  double R[8][8];
+  double R[8][2];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int i = 8 * p + r;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int k = 8 * q + c;
+    for (int c = 0; c < 2; ++c) {
+      const int k = k0 + c;
       R[r][c] = (i < n && k < n) ? (k <= i ? Ab[i * C + k] : 0.0) : (i == k ? 1.0 : 0.0);
     }
   }
@@ -117,42 +119,38 @@ __global__ void __launch_bounds__(64)
   bool ok = true;
 #pragma unroll 1
   for (int jp = 7; jp >= 0; --jp) {
-    const bool own_row = (p == jp), own_col = (q == jp);
+    const bool own_row = (p == jp);
 #pragma unroll
     for (int jr = 7; jr >= 0; --jr) {
       const int j = 8 * jp + jr;
-      if (own_row) {  // the 8 lanes holding row j publish it
+      double* row = bc[jr & 1];
+      if (own_row) *reinterpret_cast<f64x2_t*>(row + k0) = f64x2_t{R[jr][0], R[jr][1]};
+      __syncthreads();
+      double ai[8];
 #pragma unroll
-        for (int c = 0; c < 8; c += 2)
-          *reinterpret_cast<f64x2_t*>(bc + 8 * q + c) = f64x2_t{R[jr][c], R[jr][c + 1]};
+      for (int r = 0; r < 8; r += 2) {
+        const f64x2_t u = *reinterpret_cast<const f64x2_t*>(row + 8 * p + r);
+        ai[r] = u.x, ai[r + 1] = u.y;
       }
-      __builtin_amdgcn_wave_barrier();
-      double ai[8], ak[8];
-#pragma unroll
-      for (int c = 0; c < 8; c += 2) {
-        const f64x2_t u = *reinterpret_cast<const f64x2_t*>(bc + 8 * p + c);
-        const f64x2_t v = *reinterpret_cast<const f64x2_t*>(bc + 8 * q + c);
-        ai[c] = u.x, ai[c + 1] = u.y, ak[c] = v.x, ak[c + 1] = v.y;
-      }
-      const double d = bc[j];
-      __builtin_amdgcn_wave_barrier();
+      const f64x2_t ak = *reinterpret_cast<const f64x2_t*>(row + k0);
+      const double d = row[j];
       ok = ok & (d > 0.0);
       const double rd = recip_f64(d);
       piv[jr] = own_row ? d : piv[jr];
-      double cf[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) cf[r] = (8 * p + r < j) ? ai[r] * rd : 0.0;
+      const bool col_j = (k0 == (j & ~1));  // this lane holds column j
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) R[r][c] = fma(-cf[r], ak[c], R[r][c]);
-        // column j of the inverse: X[i][j] = -c_i (cf is 0 for rows i >= j)
-        if (8 * p + r < j) R[r][jr] = own_col ? -cf[r] : R[r][jr];
+        const bool upd = 8 * p + r < j;
+        const double cf = upd ? ai[r] * rd : 0.0;
+        R[r][0] = fma(-cf, ak.x, R[r][0]);
+        R[r][1] = fma(-cf, ak.y, R[r][1]);
+        // column j of the inverse: X[i][j] = -c_i
+        if (upd && col_j) R[r][j & 1] = -cf;
       }
     }
   }
   if (!__builtin_amdgcn_readfirstlane(ok ? 1 : 0)) {  // d is the same in every lane
-    if (lane == 0) failed[b] = 1;
+    if (threadIdx.x == 0) failed[b] = 1;
     return;
   }
   double* Wb = W + b * C * C + r0 * C + r0;
@@ -162,8 +160,8 @@ __global__ void __launch_bounds__(64)
     if (i >= n) continue;
     const double rs = 1.0 / sqrt(piv[r]);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int k = 8 * q + c;
+    for (int c = 0; c < 2; ++c) {
+      const int k = k0 + c;
       if (k < n) Wb[i * C + k] = k > i ? R[r][c] * rs : (k == i ? rs : 0.0);
     }
   }
@@ -363,7 +361,7 @@ int factor_rec(const Ctx& x, int64_t b0, int64_t b1, int depth) {
   const int64_t C = x.C, CC = C * C;
   const int64_t r0 = b0 * kNb, r1 = std::min(b1 * kNb, C);
   if (b1 - b0 == 1) {
-    leaf_kernel<<<static_cast<unsigned>(x.B), 64, 0, x.s>>>(x.A, x.W, C, r0,
+    leaf_kernel<<<static_cast<unsigned>(x.B), 256, 0, x.s>>>(x.A, x.W, C, r0,
                                                             static_cast<int>(r1 - r0), x.active,
                                                             x.failed);
     return check_launch("hinv leaf");

@@ -354,9 +354,15 @@ __global__ void __launch_bounds__(kWaves * 64)
   }
 }
 
-// W[row, i2 + m] -= sum_k Err[row, k] * U[b, i1 + k, i2 + m]: 64x64 output
-// tiles, K = n staged through LDS in chunks of 32.
-constexpr int kTm = 64, kTn = 64, kTk = 32;
+// W[row, i2 + m] -= sum_k Err[row, k] * U[b, i1 + k, i2 + m] (the reference's
+// deferred bmm): 64x64 output tiles, each wave a 32x32 block on
+// v_mfma_f32_32x32x2f32 (A[l%32][k], B[k][l%32] with k = l/32 per step; result
+// register r of lane l = D[8(r/4) + 4(l/32) + r%4][l%32]). Each lane loads
+// four consecutive k of its Err row with one 16-byte load and the matching
+// four U rows; step t of a chunk of 8 takes k = chunk + 4(l/32) + t for both
+// operands (the same permutation of k).
+constexpr int kTm = 64, kTn = 64;
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 __global__ void __launch_bounds__(256)
     lazy_update_kernel(float* __restrict__ W, const float* __restrict__ U,
@@ -364,50 +370,44 @@ __global__ void __launch_bounds__(256)
                        int n) {
   const int64_t i2 = i1 + n;
   const int64_t b = blockIdx.z;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTm;
-  const int64_t m0 = i2 + static_cast<int64_t>(blockIdx.x) * kTn;
-  if (r0 >= R || m0 >= C) return;
-  __shared__ float Es[kTm][kTk + 1];
-  __shared__ float Us[kTk][kTn + 1];
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;  // 4x4 outputs per thread
-  float acc[4][4] = {};
-  const float* Ub = U + b * C * C;
-  for (int k0 = 0; k0 < n; k0 += kTk) {
-    for (int e = threadIdx.x; e < kTm * kTk; e += 256) {
-      const int rr = e / kTk, kk = e % kTk;
-      const int64_t r = r0 + rr;
-      Es[rr][kk] = (r < R && k0 + kk < n) ? Err[(b * R + r) * n + k0 + kk] : 0.0f;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTm + (wave >> 1) * 32;
+  const int64_t m0 = i2 + static_cast<int64_t>(blockIdx.x) * kTn + (wave & 1) * 32;
+  if (r0 >= R || m0 >= C) return;  // whole wave
+  const int li = lane & 31, g = lane >> 5;
+  const int64_t r = r0 + li, m = m0 + li;
+  const bool rok = r < R, mok = m < C;
+  const float* Ea = Err + (b * R + (rok ? r : 0)) * n;
+  const float* Ubk = U + b * C * C + i1 * C + (mok ? m : i2);
+  const bool vec = (n & 3) == 0;
+  f32x16_t acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  for (int kc = 0; kc < n; kc += 8) {
+    const int kb = kc + 4 * g;
+    float a[4], u[4];
+    if (vec && kb + 4 <= n) {
+      const float4 v = *reinterpret_cast<const float4*>(Ea + kb);
+      a[0] = v.x, a[1] = v.y, a[2] = v.z, a[3] = v.w;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = kb + t < n ? Ea[kb + t] : 0.0f;
     }
-    for (int e = threadIdx.x; e < kTk * kTn; e += 256) {
-      const int kk = e / kTn, mm = e % kTn;
-      const int64_t m = m0 + mm;
-      Us[kk][mm] = (m < C && k0 + kk < n) ? Ub[(i1 + k0 + kk) * C + m] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) u[t] = kb + t < n ? Ubk[static_cast<int64_t>(kb + t) * C] : 0.0f;
+    if (!rok) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = 0.0f;
     }
-    __syncthreads();
-    for (int kk = 0; kk < kTk; ++kk) {
-      float ev[4], uv[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) ev[a] = Es[ty * 4 + a][kk];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) uv[a] = Us[kk][tx * 4 + a];
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int c2 = 0; c2 < 4; ++c2) acc[a][c2] = fmaf(ev[a], uv[c2], acc[a][c2]);
-    }
-    __syncthreads();
+    for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], u[t], acc, 0, 0, 0);
   }
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t r = r0 + ty * 4 + a;
-    if (r >= R) continue;
-#pragma unroll
-    for (int c2 = 0; c2 < 4; ++c2) {
-      const int64_t m = m0 + tx * 4 + c2;
-      if (m < C) {
-        float* p = W + (b * R + r) * C + m;
-        *p = *p - acc[a][c2];
-      }
+  for (int i = 0; i < 16; ++i) {
+    const int64_t rr = r0 + 8 * (i >> 2) + 4 * g + (i & 3);
+    if (rr < R && mok) {
+      float* p = W + (b * R + rr) * C + m;
+      *p = *p - acc[i];
     }
   }
 }
