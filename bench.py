@@ -39,6 +39,7 @@ sys.path.insert(0, os.path.join(ROOT, "mlx-gptq-mxfp_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0
+PEAK_FP64_TFLOPS = 78.6  # MI355X fp64 (vector and matrix)
 MXFP_BYTES_PER_ELEMENT = 2 + 4 + 1 + 1 / 32  # bf16 W in, f32 W_dq + u8 code out, E8M0 scale
 
 
@@ -72,9 +73,11 @@ def _traffic(name: str, kernel_prefix: str):
 
 
 def _roofline(kernel, bound, amount, ms, traffic=None):
-    """amount: flops (bound "mfma") or bytes (bound "hbm") per launch."""
-    if bound == "mfma":
-        achieved, peak, unit = amount / (ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+    """amount: flops (bound "mfma": bf16 MFMA peak; "fp64": fp64 peak) or bytes
+    (bound "hbm") per launch."""
+    if bound in ("mfma", "fp64"):
+        peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_FP64_TFLOPS
+        achieved, unit = amount / (ms * 1e-3) / 1e12, "TFLOP/s"
     else:
         achieved, peak, unit = amount / (ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
     return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak,
@@ -286,9 +289,18 @@ def run_dense(args, torch, np) -> int:
         phases[f"solve_{m.name}"] = ms
         n = int(m.W.numel())
         if m.solve["mode"] == "affine":
-            byt = n * (2 + 4 + 1 + 4 / m.solve["group_size"])
-        else:
-            byt = n * MXFP_BYTES_PER_ELEMENT
+            # O(C^3) work: the fp64 factor + inverse (2C^3/3 algorithmic, potrf +
+            # trtri) and the deferred fp32 update 2 R sum_blocks bs (C - i2),
+            # framed against the fp64 peak (the serial pivot and column chains
+            # bound it, not HBM)
+            R_, C_ = m.W.shape[-2], m.W.shape[-1]
+            bs = 128
+            upd = sum(2 * R_ * min(bs, C_ - i) * (C_ - min(i + bs, C_)) for i in range(0, C_, bs))
+            rooflines[f"solve_{m.name}"] = _roofline(
+                f"GPTQ solve '{m.name}' (affine: fp64 Cholesky-inverse + column loop + fp32 lazy update)",
+                "fp64", 2 * C_ ** 3 / 3 + upd, ms)
+            continue
+        byt = n * MXFP_BYTES_PER_ELEMENT
         rooflines[f"solve_{m.name}"] = _roofline(f"GPTQ solve '{m.name}' ({m.solve['mode']})", "hbm",
                                                  byt, ms)
     phases["pack"] = phase[-1]
