@@ -419,10 +419,14 @@ __global__ void zero_fill_kernel(uint32_t* __restrict__ p, int64_t n_words) {
 }
 
 // Sum the K-split partial tiles of one output tile in slot order and write
-// the lower triangle (+ mirror) of H. One block per 64x64 sub-tile: partial
-// rows are read and H rows written along the fast index, and the mirrored
-// values go out through an LDS transpose, so both stores are coalesced.
+// the lower triangle (+ mirror) of H. One block per 64x64 sub-tile: thread
+// (rr = tid / 16, c4 = 4 (tid % 16)) takes columns c4..c4+3 of rows rr,
+// rr+16, rr+32, rr+48 with 16-byte loads, the slots of a row loaded eight
+// at a time before they are added (in slot order, so H is deterministic);
+// the mirrored values go out through an LDS transpose, so both stores are
+// coalesced.
 constexpr int kRedSub = 64;
+constexpr int kRedSlots = 8;
 __global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __restrict__ tiles,
                                                            const float* __restrict__ partials,
                                                            float* __restrict__ H, int64_t C,
@@ -433,24 +437,51 @@ __global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __re
   const int sr = blockIdx.x / (kTile / kRedSub), sc = blockIdx.x % (kTile / kRedSub);
   const int64_t bi = static_cast<int64_t>(st.ti) * kTile + sr * kRedSub;  // global row base
   const int64_t bj = static_cast<int64_t>(st.tj) * kTile + sc * kRedSub;  // global column base
-  const int c = threadIdx.x & (kRedSub - 1), r0 = threadIdx.x / kRedSub;
+  const int c4 = (threadIdx.x & 15) * 4, rr = threadIdx.x >> 4;
   const float* p0 = partials + static_cast<int64_t>(st.slot0) * kTile * kTile;
-#pragma unroll 4
-  for (int r = r0; r < kRedSub; r += 256 / kRedSub) {
-    const int e = (sr * kRedSub + r) * kTile + sc * kRedSub + c;
-    float v = p0[e];
-    for (int s = 1; s < st.nslots; ++s) v += p0[static_cast<int64_t>(s) * kTile * kTile + e];
-    const int64_t gi = bi + r, gj = bj + c;
-    float nv = v;
-    if (gi < C && gj < C && gi >= gj) {
-      float* p = Hg + gi * C + gj;
-      nv = accumulate ? (*p + v) : v;
-      *p = nv;
+  constexpr int64_t kSlot = static_cast<int64_t>(kTile) * kTile;
+#pragma unroll
+  for (int qr = 0; qr < kRedSub / 16; ++qr) {
+    const int r = rr + 16 * qr;
+    const int e = (sr * kRedSub + r) * kTile + sc * kRedSub + c4;
+    float4 v = *reinterpret_cast<const float4*>(p0 + e);
+    for (int s0 = 1; s0 < st.nslots; s0 += kRedSlots) {
+      float4 t[kRedSlots];
+#pragma unroll
+      for (int i = 0; i < kRedSlots; ++i)
+        if (s0 + i < st.nslots) t[i] = *reinterpret_cast<const float4*>(p0 + (s0 + i) * kSlot + e);
+#pragma unroll
+      for (int i = 0; i < kRedSlots; ++i)
+        if (s0 + i < st.nslots) {
+          v.x += t[i].x;
+          v.y += t[i].y;
+          v.z += t[i].z;
+          v.w += t[i].w;
+        }
     }
-    tr[c][r] = nv;
+    const int64_t gi = bi + r, gj = bj + c4;
+    float nv[4] = {v.x, v.y, v.z, v.w};
+    float* p = Hg + gi * C + gj;
+    if (gi < C && gj + 3 < C && gi >= gj + 3) {  // four lower-triangle entries
+      if (accumulate) {
+        const float4 h = *reinterpret_cast<const float4*>(p);
+        nv[0] += h.x, nv[1] += h.y, nv[2] += h.z, nv[3] += h.w;
+      }
+      *reinterpret_cast<float4*>(p) = float4{nv[0], nv[1], nv[2], nv[3]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (gi < C && gj + k < C && gi >= gj + k) {
+          nv[k] = accumulate ? p[k] + nv[k] : nv[k];
+          p[k] = nv[k];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tr[c4 + k][r] = nv[k];
   }
   __syncthreads();
   // mirror: H[bj + r][bi + c] = value of (bi + c, bj + r), strictly below the diagonal
+  const int c = threadIdx.x & (kRedSub - 1), r0 = threadIdx.x / kRedSub;
 #pragma unroll 4
   for (int r = r0; r < kRedSub; r += 256 / kRedSub) {
     const int64_t gi = bi + c, gj = bj + r;
