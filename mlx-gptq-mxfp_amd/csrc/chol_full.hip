@@ -87,10 +87,14 @@ __global__ void build_kernel(const float* __restrict__ H, int64_t C, const float
 // after its step; at the end W[i][k] = R[i][k] / sqrt(d_i) for k > i and
 // W[i][i] = 1 / sqrt(d_i). Wave w holds columns 16w..16w+15, its lanes an
 // 8 x 8 grid (p = lane / 8, q = lane % 8): lane (p, q) holds rows 8p..8p+7 x
-// columns 16w + 2q, 16w + 2q + 1 (16 fp64 registers). Each step the lanes
-// holding row j publish it through LDS (two alternating buffers, so one
-// workgroup barrier per step) and every lane reads the 8 entries of its
-// rows, its 2 columns and the pivot: 16 FMAs per lane-step. Only the lower
+// columns 16w + 2q, 16w + 2q + 1 (16 fp64 registers). The steps go in pairs
+// (j, j - 1), both rows in the same 8-row group: the lanes holding the two
+// rows publish them through LDS (two alternating buffer pairs, so one
+// workgroup barrier per pair), and every lane forms row j - 1 after step j
+// from the two published rows itself, with the same operations the lanes
+// holding row j - 1 apply to it (so the result is bitwise that of single
+// steps). Each lane reads the entries of its 8 rows, its 2 columns and the
+// pivots of both rows: 32 FMAs of update per lane and pair. Only the lower
 // triangle of the block is read; rows past n are identity padding. A pivot
 // <= 0 or NaN flags the item as failed.
 __global__ void __launch_bounds__(256)
@@ -98,7 +102,7 @@ __global__ void __launch_bounds__(256)
                 const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
   const int64_t b = blockIdx.x;
   if (!active[b] || failed[b]) return;  // uniform over the workgroup
-  __shared__ __attribute__((aligned(16))) double bc[2][kNb];
+  __shared__ __attribute__((aligned(16))) double bc[4][kNb];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int p = lane >> 3, q = lane & 7;
   const int k0 = 16 * wave + 2 * q;  // this lane's two columns
@@ -121,23 +125,37 @@ __global__ void __launch_bounds__(256)
   for (int jp = 7; jp >= 0; --jp) {
     const bool own_row = (p == jp);
 #pragma unroll
-    for (int jr = 7; jr >= 0; --jr) {
-      const int j = 8 * jp + jr;
-      double* row = bc[jr & 1];
-      if (own_row) *reinterpret_cast<f64x2_t*>(row + k0) = f64x2_t{R[jr][0], R[jr][1]};
+    for (int jr = 7; jr >= 1; jr -= 2) {
+      const int j = 8 * jp + jr;  // pivots j, then j - 1
+      double* rj = bc[2 * ((jr >> 1) & 1)];
+      double* rj1 = rj + kNb;
+      if (own_row) {
+        *reinterpret_cast<f64x2_t*>(rj + k0) = f64x2_t{R[jr][0], R[jr][1]};
+        *reinterpret_cast<f64x2_t*>(rj1 + k0) = f64x2_t{R[jr - 1][0], R[jr - 1][1]};
+      }
       __syncthreads();
-      double ai[8];
+      double ai[8], bi[8];
 #pragma unroll
       for (int r = 0; r < 8; r += 2) {
-        const f64x2_t u = *reinterpret_cast<const f64x2_t*>(row + 8 * p + r);
+        const f64x2_t u = *reinterpret_cast<const f64x2_t*>(rj + 8 * p + r);
+        const f64x2_t v = *reinterpret_cast<const f64x2_t*>(rj1 + 8 * p + r);
         ai[r] = u.x, ai[r + 1] = u.y;
+        bi[r] = v.x, bi[r + 1] = v.y;
       }
-      const f64x2_t ak = *reinterpret_cast<const f64x2_t*>(row + k0);
-      const double d = row[j];
-      ok = ok & (d > 0.0);
+      const f64x2_t ak = *reinterpret_cast<const f64x2_t*>(rj + k0);
+      const f64x2_t bk = *reinterpret_cast<const f64x2_t*>(rj1 + k0);
+      const f64x2_t dj = *reinterpret_cast<const f64x2_t*>(rj + j - 1);  // {a_{j-1}, d}
+      const double e = rj1[j - 1];
+      const double d = dj.y;
       const double rd = recip_f64(d);
+      const double cj = dj.x * rd;           // c_{j-1} of step j
+      const double d1 = fma(-cj, dj.x, e);   // pivot of step j - 1
+      ok = ok & (d > 0.0) & (d1 > 0.0);
+      const double rd1 = recip_f64(d1);
       piv[jr] = own_row ? d : piv[jr];
-      const bool col_j = (k0 == (j & ~1));  // this lane holds column j
+      piv[jr - 1] = own_row ? d1 : piv[jr - 1];
+      const bool col_j = (k0 == j - 1);  // this lane holds columns j - 1 and j
+      // step j
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const bool upd = 8 * p + r < j;
@@ -145,7 +163,22 @@ __global__ void __launch_bounds__(256)
         R[r][0] = fma(-cf, ak.x, R[r][0]);
         R[r][1] = fma(-cf, ak.y, R[r][1]);
         // column j of the inverse: X[i][j] = -c_i
-        if (upd && col_j) R[r][j & 1] = -cf;
+        R[r][1] = (upd && col_j) ? -cf : R[r][1];
+      }
+      // row j - 1 after step j, at this lane's rows and columns
+      double a1[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) a1[r] = fma(-cj, ai[r], bi[r]);
+      const double ak1x = fma(-cj, ak.x, bk.x);
+      const double ak1y = col_j ? -cj : fma(-cj, ak.y, bk.y);
+      // step j - 1
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const bool upd = 8 * p + r < j - 1;
+        const double cf = upd ? a1[r] * rd1 : 0.0;
+        R[r][0] = fma(-cf, ak1x, R[r][0]);
+        R[r][1] = fma(-cf, ak1y, R[r][1]);
+        R[r][0] = (upd && col_j) ? -cf : R[r][0];
       }
     }
   }
