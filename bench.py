@@ -55,6 +55,10 @@ def _args(argv=None):
                     help="before the steps, run one plain elementwise copy (torch.neg) of this many "
                          "MiB: the reference dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE "
                          "to bytes")
+    ap.add_argument("--capture", action="store_true",
+                    help="config 4 only: time the routed capture path instead of the solve "
+                         "(per-batch RoutedStash.add_routed, plan, one grouped Hessian launch), "
+                         "with the reference's per-expert CPU stash path timed beside it")
     return ap.parse_args(argv)
 
 
@@ -192,6 +196,102 @@ def run_moe(args, torch, np) -> int:
     phases = {"hessian_gate_up": phase[0], "hessian_down": phase[1], "solve_gate_up": phase[2],
               "solve_down": phase[3], "rtn_and_pack": phase[4]}
     _line(args, value, ms_step, config, phases, roofline, cpu, setup_s)
+    return 0
+
+
+def run_capture(args, torch, np) -> int:
+    """Routed capture of the config-4 layer's gate_up inputs: 64 batches of
+    2048 tokens, each stashed once with its top-8 expert ids, then every
+    expert's H from one grouped launch. The reference's path (one CPU bf16
+    Stash per expert filled with the gathered rows, capture.py:42-50, then
+    per-expert fp32 addmm on the GPU, capture.py:68-76) is timed beside it on
+    the first batches."""
+    from mlx_gptq import capture, synth
+
+    dev = torch.device("cuda", 0)
+    t_setup = time.perf_counter()
+    L = synth.moe_layer(device=dev)
+    E, T = L.experts, L.X.shape[0]
+    hidden = L.X.shape[1]
+    counts = torch.tensor(L.counts(), device=dev)
+    expert_of = torch.repeat_interleave(torch.arange(E, device=dev), counts)
+    order = torch.argsort(L.row_index.long(), stable=True)
+    top_k = expert_of[order].reshape(T, -1)  # the router's choice per token
+    K = top_k.shape[1]
+    bt = 2048
+    batches = [(a, min(a + bt, T)) for a in range(0, T, bt)]
+    H = torch.empty(E, hidden, hidden, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    stash = capture.RoutedStash("gate_up", hidden, E)
+
+    def step():
+        stash.clear()
+        evs[0].record()
+        for a, b in batches:
+            stash.add_routed(L.X[a:b], top_k[a:b])
+        evs[1].record()
+        stash.plan()
+        evs[2].record()
+        stash.hessians(out=H)
+        evs[3].record()
+        return H, evs
+
+    out, ms_step, phase = _timed(torch, np, step, 3, args.warmup, args.steps)
+    A = T * K
+    # parity with the solve path's Hessians (same rows, other order)
+    H_ref = capture.grouped_hessian(L.X, L.offsets, L.row_index)
+    rel = float(((out - H_ref).norm() / H_ref.norm()).item())
+    roofline = _roofline("syrk_kernel (gate_up Hessian, routed gather)", "mfma", A * hidden * (hidden + 1),
+                         float(phase[2]), _traffic("bench_moe_cfg4", "mgq::syrk_kernel<true"))
+    # the reference's per-expert stash path on the first batches (skipped
+    # with --cpu-seconds 0)
+    nb = min(len(batches), 4)
+    ref = None
+    if args.cpu_seconds > 0:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        stashes = [[] for _ in range(E)]
+        for a, b in batches[:nb]:
+            xb, tb = L.X[a:b], top_k[a:b]
+            for e in range(E):
+                tok = torch.nonzero((tb == e).any(dim=1)).flatten()
+                if tok.numel():
+                    stashes[e].append(xb[tok].to("cpu", torch.bfloat16))
+        t1 = time.perf_counter()
+        for e in range(E):
+            Hm = torch.zeros(hidden, hidden, dtype=torch.float32, device=dev)
+            for c in stashes[e]:
+                x = c.to(dev, torch.float32, non_blocking=True)
+                Hm.addmm_(x.T, x)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        a_ref = sum(b - a for a, b in batches[:nb]) * K
+        ref = {"value": round(a_ref / (t2 - t0), 1), "unit": "assignments/s",
+               "kind": "reference path (torch, GPU + host copies)",
+               "sample": f"first {nb} of {len(batches)} batches: per-expert gather + copy to CPU bf16 "
+                         f"{(t1 - t0) * 1e3:.1f} ms, per-expert fp32 addmm Hessians "
+                         f"{(t2 - t1) * 1e3:.1f} ms",
+               "cores": torch.get_num_threads()}
+    line = {
+        "metric": "routed-capture assignments/s (stash + plan + grouped Hessian)",
+        "value": round(A / (ms_step * 1e-3), 1),
+        "unit": "assignments/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16+fp32",
+        "data": "synthetic (config-4 hidden states and top-8 routing)",
+        "config": {"workload": f"cfg4 gate_up capture: {T} tokens in {len(batches)} batches of {bt}, "
+                               f"top-{K} of {E} experts, hidden {hidden}",
+                   "assignments": A},
+        "phases_ms": {"add_routed": round(float(phase[0]), 3), "plan": round(float(phase[1]), 3),
+                      "hessian": round(float(phase[2]), 3)},
+        "roofline": roofline,
+        "rel_frobenius_vs_solve_path_hessians": rel,
+        "reference_path": ref,
+        "setup_s": round(setup_s, 2),
+    }
+    print(json.dumps(line), flush=True)
     return 0
 
 
@@ -384,6 +484,11 @@ def main(argv=None) -> int:
 
     _native.load()
     torch.cuda.set_device(torch.device("cuda", 0))
+    if args.capture:
+        if args.config != 4:
+            print("--capture measures the routed (config 4) layer only", file=sys.stderr)
+            return 2
+        return run_capture(args, torch, np)
     if args.config == 4:
         return run_moe(args, torch, np)
     return run_dense(args, torch, np)

@@ -11,6 +11,14 @@ formed: one bf16-MFMA SYRK launch (csrc/hessian.hip) instead of chunked fp32
 ``grouped_hessian`` is the batched form used for routed experts: every
 expert's H from one hidden-state matrix plus a per-expert token list, with
 the gather fused into the MFMA tile loads.
+
+``RoutedStash`` and ``ExpertCapture`` are the routed-capture side of it
+(the reference keeps one CPU ``Stash`` per expert, filled by intercepting
+``F.linear`` on each expert's weight slice, capture.py:101-207): a fused
+MoE expert module's input is stashed once per batch together with the
+router's top-k assignment, so an expert's rows are never copied out; rows
+that exist only per expert (the ``down_proj`` inputs) are appended with
+their expert id. Every expert's H then comes from one grouped launch.
 """
 
 from __future__ import annotations
@@ -20,8 +28,15 @@ from typing import Sequence
 
 import numpy as np
 import torch
+import torch.nn.functional as F
+from torch.overrides import TorchFunctionMode
 
 from . import _native as nat
+
+# 3D expert parameter names of the transformers fused-expert layout
+# (capture.py:28); the first three take the MoE block's hidden states.
+FUSED_EXPERT_PARAMS = ("gate_up_proj", "gate_proj", "up_proj", "down_proj")
+_INPUT_PARAMS = ("gate_up_proj", "gate_proj", "up_proj")
 
 
 def _as_offsets(offsets) -> np.ndarray:
@@ -124,8 +139,9 @@ class Stash:
                 f"stash {self.name}: got rows of dim {rows.shape[-1]}, "
                 f"expected {self.in_features}"
             )
-        # bf16 rounding as capture.py:49; rows stay on their device.
-        self.chunks.append(rows.to(torch.bfloat16).contiguous())
+        # bf16 rounding as capture.py:49; rows stay on their device, in a
+        # copy of their own (the caller may reuse its input buffer).
+        self.chunks.append(rows.to(torch.bfloat16, copy=True).contiguous())
         self.tokens += rows.shape[0]
 
     def add_sampled(self, x: torch.Tensor, max_rows: int):
@@ -164,3 +180,291 @@ class Stash:
 
     def clear(self):
         self.chunks.clear()
+
+
+class RoutedStash:
+    """Calibration rows of every expert of one fused [E, out, in] parameter.
+
+    Holds what the reference keeps as E per-expert stashes (keys
+    ``{module}.{param}::e{e}``, capture.py:149-153, each filled with the rows
+    routed to that expert, capture.py:192-207) as one append-only bf16 row
+    buffer on the capture device plus an (expert, row) assignment list:
+
+    * ``add_routed(x, top_k_index)``: the block's input rows, stored once,
+      and the router's choice for each (expert ids outside [0, E) are
+      dropped, as the eager expert loop skips them);
+    * ``add_rows(expert, x)``: rows that exist for one expert only (the
+      ``down_proj`` inputs).
+
+    ``hessians`` forms H_e = X_e^T X_e (fp32) for a span of experts in one
+    grouped SYRK launch, gathering each expert's rows inside the kernel.
+    Rows are rounded to bf16 as capture.py:49 does; the row order inside
+    an expert differs from the eager loop's, which changes only the fp32
+    summation order of H.
+    """
+
+    def __init__(self, name: str, in_features: int, num_experts: int):
+        self.name = name
+        self.in_features = int(in_features)
+        self.num_experts = int(num_experts)
+        self.chunks: list[torch.Tensor] = []
+        self._experts: list[torch.Tensor] = []  # int32 expert id per assignment
+        self._rows: list[torch.Tensor] = []  # int32 row of the buffer per assignment
+        self.rows = 0  # rows stored
+        self._plan = None
+
+    def _append(self, x: torch.Tensor) -> tuple[torch.Tensor, int]:
+        rows = x.detach().reshape(-1, x.shape[-1])
+        if rows.shape[-1] != self.in_features:
+            raise RuntimeError(
+                f"stash {self.name}: got rows of dim {rows.shape[-1]}, "
+                f"expected {self.in_features}"
+            )
+        base = self.rows
+        if base + rows.shape[0] > 2**31 - 1:
+            raise RuntimeError(f"stash {self.name}: more than 2^31 - 1 rows")
+        self.chunks.append(rows.to(torch.bfloat16, copy=True).contiguous())
+        self.rows += rows.shape[0]
+        self._plan = None
+        return rows, base
+
+    def add_routed(self, x: torch.Tensor, top_k_index: torch.Tensor):
+        """Rows x [T, C] (any leading shape) routed to experts
+        top_k_index [T, k] (the router's top-k choice per row)."""
+        rows, base = self._append(x)
+        T = rows.shape[0]
+        ti = top_k_index.detach()
+        if ti.dtype.is_floating_point or ti.numel() % max(T, 1) != 0:
+            raise ValueError(f"stash {self.name}: top_k_index must hold k integer ids per row")
+        ti = ti.reshape(T, -1).to(device=rows.device)
+        k = ti.shape[1]
+        e = ti.reshape(-1).to(torch.int64)
+        e = torch.where((e >= 0) & (e < self.num_experts), e, self.num_experts).to(torch.int32)
+        r = (torch.arange(T, device=rows.device, dtype=torch.int32) + base).repeat_interleave(k)
+        self._experts.append(e)
+        self._rows.append(r)
+
+    def add_rows(self, expert: int, x: torch.Tensor):
+        """Rows x that belong to `expert` alone."""
+        if not 0 <= int(expert) < self.num_experts:
+            raise IndexError(f"stash {self.name}: expert {expert} outside [0, {self.num_experts})")
+        rows, base = self._append(x)
+        n = rows.shape[0]
+        self._experts.append(torch.full((n,), int(expert), dtype=torch.int32, device=rows.device))
+        self._rows.append(torch.arange(base, base + n, dtype=torch.int32, device=rows.device))
+
+    def nbytes(self) -> int:
+        return sum(c.numel() * 2 for c in self.chunks) + sum(r.numel() * 8 for r in self._rows)
+
+    def plan(self) -> tuple[torch.Tensor, np.ndarray, torch.Tensor]:
+        """(X, offsets, row_index): X bf16 [rows, C], the stored rows;
+        expert e's rows are X[row_index[offsets[e]:offsets[e + 1]]]
+        (offsets int64 [E + 1] on the host, row_index int32 on X's device).
+        One host sync (the per-expert counts)."""
+        if self._plan is None:
+            if not self.chunks:
+                raise RuntimeError(f"stash {self.name}: nothing captured")
+            X = self.chunks[0] if len(self.chunks) == 1 else torch.cat(self.chunks)
+            self.chunks = [X]
+            e = torch.cat(self._experts)
+            r = torch.cat(self._rows)
+            e_sorted, order = torch.sort(e, stable=True)
+            row_index = r[order].contiguous()
+            counts = torch.bincount(e_sorted, minlength=self.num_experts + 1)[: self.num_experts]
+            off = np.zeros(self.num_experts + 1, dtype=np.int64)
+            off[1:] = np.cumsum(counts.cpu().numpy())
+            self._experts, self._rows = [e_sorted], [row_index]
+            self._plan = (X, off, row_index)
+        return self._plan
+
+    def token_counts(self) -> np.ndarray:
+        """Rows per expert (int64 [E])."""
+        if not self.chunks:
+            return np.zeros(self.num_experts, dtype=np.int64)
+        return np.diff(self.plan()[1])
+
+    def expert_rows(self, expert: int) -> torch.Tensor:
+        """Expert `expert`'s rows, gathered (bf16 [n, C])."""
+        X, off, ri = self.plan()
+        return X.index_select(0, ri[int(off[expert]) : int(off[expert + 1])].long())
+
+    @torch.no_grad()
+    def hessians(self, device=None, experts: range | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """H_e = X_e^T X_e, fp32 [len(experts), C, C], for experts
+        e0..e1-1 (default: all), as sequential.py:546-551 stacks per-expert
+        Stash.hessian results; experts without rows get H = 0."""
+        E = self.num_experts
+        experts = range(E) if experts is None else experts
+        if experts.step != 1 or not 0 <= experts.start <= experts.stop <= E:
+            raise ValueError(f"experts must be a contiguous span inside [0, {E})")
+        C = self.in_features
+        if not self.chunks:
+            dev = torch.device(device) if device is not None else None
+            if dev is None or dev.type != "cuda":
+                raise RuntimeError("mlx_gptq (MI355X build) accumulates Hessians on HIP devices only")
+            return torch.zeros(len(experts), C, C, dtype=torch.float32, device=dev)
+        X, off, ri = self.plan()
+        if device is not None:
+            dev = torch.device(device)
+            if dev.type != "cuda":
+                raise RuntimeError(
+                    "mlx_gptq (MI355X build) accumulates Hessians on HIP devices only "
+                    f"(got device {dev})"
+                )
+            if X.device != dev:
+                X, ri = X.to(dev), ri.to(dev)
+                self.chunks, self._rows = [X], [ri]
+                self._plan = (X, off, ri)
+        return grouped_hessian(X, off[experts.start : experts.stop + 1], ri, out=out,
+                               validate=False)
+
+    def hessian(self, expert: int, device=None) -> torch.Tensor:
+        """One expert's H (fp32 [C, C]), the per-expert Stash.hessian."""
+        return self.hessians(device, range(int(expert), int(expert) + 1))[0]
+
+    def clear(self):
+        self.chunks.clear()
+        self._experts.clear()
+        self._rows.clear()
+        self.rows = 0
+        self._plan = None
+
+
+class ExpertCapture:
+    """Routed capture of every fused MoE expert parameter under `root`.
+
+    Finds the modules that own 3D ``gate_up_proj`` / ``gate_proj`` /
+    ``up_proj`` / ``down_proj`` parameters [E, out, in] (the detection of
+    capture.py:133-158) and gives each parameter a ``RoutedStash``
+    (``stashes["{module}.{param}"]``; the input parameters of one module
+    share one). While active:
+
+    * a forward pre-hook on each such module stashes its input
+      (``hidden_states``) once, with the ``top_k_index`` it is called with
+      (the transformers expert-module signature ``forward(hidden_states,
+      top_k_index, top_k_weights)``);
+    * a TorchFunctionMode matches ``F.linear`` weights against each expert
+      slice's data pointer, as capture.py:192-207 does, and appends the
+      ``down_proj`` inputs to expert e's rows. For a module called without
+      a usable ``top_k_index`` the input parameters are captured the same
+      way (rows copied per expert, still on device).
+    """
+
+    def __init__(self, root: torch.nn.Module, group_size: int | None = None):
+        self.stashes: dict[str, RoutedStash] = {}
+        self.params: dict[str, tuple[str, str, torch.nn.Parameter]] = {}
+        self._modules: dict[str, torch.nn.Module] = {}
+        self._input_key: dict[str, str] = {}  # module name -> shared input stash key
+        self._ptr: dict[int, tuple[str, int, str]] = {}  # slice ptr -> (key, expert, module)
+        self._routed: dict[str, bool] = {}
+        self._hooks = []
+        self._mode = None
+        self.skipped: list[str] = []
+        for name, mod in root.named_modules():
+            for pname, p in mod.named_parameters(recurse=False):
+                if p.dim() != 3 or pname not in FUSED_EXPERT_PARAMS:
+                    continue
+                key = f"{name}.{pname}" if name else pname
+                E, C = p.shape[0], p.shape[-1]
+                if group_size and C % group_size != 0:
+                    self.skipped.append(key)  # capture.py:141-146
+                    continue
+                if pname in _INPUT_PARAMS:
+                    ik = self._input_key.setdefault(name, key)
+                    if ik not in self.stashes:
+                        self.stashes[ik] = RoutedStash(f"{name}::inputs", C, E)
+                    self.stashes[key] = self.stashes[ik]
+                else:
+                    self.stashes[key] = RoutedStash(key, C, E)
+                self.params[key] = (name, pname, p)
+                self._modules[name] = mod
+                for e in range(E):
+                    ptr = p.data_ptr() + e * p.stride(0) * p.element_size()
+                    self._ptr[ptr] = (key, e, name)
+
+    # ---- hooks ----------------------------------------------------------
+
+    def _make_pre_hook(self, name: str):
+        def hook(mod, args, kwargs):
+            x = args[0] if args else kwargs.get("hidden_states")
+            ti = args[1] if len(args) > 1 else kwargs.get("top_k_index")
+            ik = self._input_key.get(name)
+            ok = (
+                ik is not None
+                and isinstance(x, torch.Tensor)
+                and isinstance(ti, torch.Tensor)
+                and not ti.dtype.is_floating_point
+                and ti.dim() >= 1
+                and x.dim() >= 1
+                and ti.numel() % max(x.numel() // x.shape[-1], 1) == 0
+            )
+            self._routed[name] = bool(ok)
+            if ok:
+                self.stashes[ik].add_routed(x, ti)
+        return hook
+
+    class _Mode(TorchFunctionMode):
+        def __init__(self, cap):
+            super().__init__()
+            self.cap = cap
+
+        def __torch_function__(self, func, types, args=(), kwargs=None):
+            kwargs = kwargs or {}
+            if func is F.linear and len(args) >= 2:
+                w = args[1]
+                if isinstance(w, torch.Tensor) and w.dim() == 2:
+                    hit = self.cap._ptr.get(w.data_ptr())
+                    if hit is not None:
+                        key, e, name = hit
+                        st = self.cap.stashes[key]
+                        is_input = self.cap.params[key][1] in _INPUT_PARAMS
+                        if w.shape[-1] == st.in_features and not (is_input and self.cap._routed.get(name)):
+                            st.add_rows(e, args[0])
+            return func(*args, **kwargs)
+
+    def __enter__(self):
+        for name, mod in self._modules.items():
+            self._hooks.append(mod.register_forward_pre_hook(self._make_pre_hook(name), with_kwargs=True))
+        if self._ptr:
+            self._mode = self._Mode(self)
+            self._mode.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        if self._mode is not None:
+            self._mode.__exit__(*exc)
+            self._mode = None
+        for h in self._hooks:
+            h.remove()
+        self._hooks.clear()
+        return False
+
+    # ---- results ----------------------------------------------------------
+
+    def hessians(self, key: str, device=None, experts: range | None = None) -> torch.Tensor:
+        """Stacked expert Hessians of parameter `key` (see RoutedStash.hessians)."""
+        return self.stashes[key].hessians(device, experts)
+
+    def expert_token_stats(self) -> dict[str, tuple[int, int, int, int]]:
+        """key -> (min, median, max, zero_count) of rows per expert
+        (capture.py:238-248)."""
+        out = {}
+        for key in self.params:
+            c = np.sort(self.stashes[key].token_counts())
+            out[key] = (int(c[0]), int(c[len(c) // 2]), int(c[-1]), int((c == 0).sum()))
+        return out
+
+    def check_capture_happened(self):
+        """Abort when a fused parameter got no rows at all (capture.py:320-330)."""
+        for key in self.params:
+            if self.stashes[key].rows == 0:
+                raise RuntimeError(
+                    f"No tokens captured for fused experts {key}. The expert loop did not "
+                    "call the module with top_k_index nor F.linear on the expert slices; "
+                    "load the model with experts_implementation='eager'."
+                )
+
+    def drop_all(self):
+        for st in self.stashes.values():
+            st.clear()
