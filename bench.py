@@ -59,6 +59,9 @@ def _args(argv=None):
                     help="config 4 only: time the routed capture path instead of the solve "
                          "(per-batch RoutedStash.add_routed, plan, one grouped Hessian launch), "
                          "with the reference's per-expert CPU stash path timed beside it")
+    ap.add_argument("--audit", action="store_true",
+                    help="config 4 only: time the fused artifact range audit over the layer's "
+                         "gate_up weights and their MXFP4 RTN codes instead of the solve")
     return ap.parse_args(argv)
 
 
@@ -295,6 +298,62 @@ def run_capture(args, torch, np) -> int:
     return 0
 
 
+def run_audit(args, torch, np) -> int:
+    """Range audit (validate_artifacts.py:21-55) of the config-4 gate_up
+    weights: bf16 [128 x 1536, 2048] source, u8 codes, E8M0 scales. One fused
+    launch reads 2 + 1 + 1/32 bytes per element."""
+    from mlx_gptq import grid, synth, validate_artifacts
+
+    dev = torch.device("cuda", 0)
+    t_setup = time.perf_counter()
+    L = synth.moe_layer(device=dev)
+    src = L.W_gate_up.reshape(-1, L.W_gate_up.shape[-1])
+    q, sb, _, _ = grid.rtn_quantize_mxfp(src, "mxfp4")
+    del L
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def step():
+        evs[0].record()
+        st = validate_artifacts.range_audit(src, q, sb, None, "mxfp4", 32)
+        evs[1].record()
+        return st, evs
+
+    st, ms_step, phase = _timed(torch, np, step, 1, args.warmup, args.steps)
+    n = src.numel()
+    nbytes = n * (2 + 1) + n // 32
+    roofline = _roofline("range_audit_kernel", "hbm", nbytes, float(phase[0]))
+    cpu = None
+    if args.cpu_seconds > 0:
+        sys.path.insert(0, ROOT)
+        from oracle import validate_ref
+
+        rows = max(1, min(src.shape[0], 8192))
+        s_c, q_c, b_c = src[:rows].cpu(), q[:rows].cpu(), sb[:rows].cpu()
+        t0 = time.perf_counter()
+        want = validate_ref.range_audit(s_c, q_c, b_c, None, "mxfp4", 32)
+        t1 = time.perf_counter()
+        got = validate_artifacts.range_audit(src[:rows], q[:rows], sb[:rows], None, "mxfp4", 32)
+        cpu = {"value": round(rows * src.shape[1] / (t1 - t0), 1), "unit": "elements/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"first {rows} rows: torch-CPU restatement of validate_artifacts.py:15-55, "
+                         f"{(t1 - t0) * 1e3:.1f} ms", "matches_gpu": got == want}
+    line = {
+        "metric": "artifact range-audit elements/s", "value": round(n / (ms_step * 1e-3), 1),
+        "unit": "elements/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 source, u8 codes, f64 ratios",
+        "data": "synthetic (config-4 gate_up weights and their MXFP4 RTN codes)",
+        "config": {"workload": f"cfg4 gate_up range audit: [{src.shape[0]}, {src.shape[1]}] bf16",
+                   "elements": n},
+        "phases_ms": {"range_audit": round(float(phase[0]), 3)},
+        "roofline": roofline, "cpu_baseline": cpu, "result": st, "setup_s": round(setup_s, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def _cpu_baseline_moe(L, ne, gpu_out, budget_s):
     """Time the CPU oracle on whole experts of the same layer until the budget
     is spent; also report code agreement with the GPU on those experts."""
@@ -484,6 +543,11 @@ def main(argv=None) -> int:
 
     _native.load()
     torch.cuda.set_device(torch.device("cuda", 0))
+    if args.audit:
+        if args.config != 4:
+            print("--audit measures the config-4 layer only", file=sys.stderr)
+            return 2
+        return run_audit(args, torch, np)
     if args.capture:
         if args.config != 4:
             print("--capture measures the routed (config 4) layer only", file=sys.stderr)

@@ -96,6 +96,18 @@ int mgq_dequantize_affine(const uint8_t* q, const void* scales, const void* bias
                           int storage_dtype, int64_t n_groups, int64_t group_size, float* out,
                           void* stream);
 
+/* validate_artifacts.py:15-68 range audit of one artifact, fused: dequantize
+ * (grid.py:154-164) and, per 32-column group, compare max|deq| with
+ * max(32 * max|source|, 2^-126), in one pass.
+ * source: [rows, cols] of source_dtype; q: u8 [rows, cols]; scales: u8 E8M0
+ * [rows, cols/32] (mxfp) or storage_dtype [rows, cols/group_size] with
+ * biases alike (affine). stats: u64[5] on the device, zeroed by the caller:
+ * [0] non-finite dequantized values, [1] groups over the limit, [2] max
+ * ratio (fp64 bits), [3] max |source| (fp32 bits), [4] max |deq| (fp32 bits). */
+int mgq_range_audit(const void* source, int source_dtype, const uint8_t* q, const void* scales,
+                    const void* biases, int storage_dtype, int mode, int64_t rows, int64_t cols,
+                    int64_t group_size, unsigned long long* stats, void* stream);
+
 /* grid.py:167-212 choose_qparams(w, bits, method, storage_dtype, grid_steps,
  * max_shrink). w: f32 [n_groups, group_len] -> s_store, b_store in
  * storage_dtype and s32, b32 f32, all [n_groups]. method: MGQ_CLIP_*. */

@@ -290,6 +290,258 @@ int check_bits(int bits) {
   return MGQ_OK;
 }
 
+
+// Range audit of one stored artifact against its source weights
+// (validate_artifacts.py:15-68), fused into one pass: every element is
+// dequantized in-register (dequantize_artifact, grid.py:154-164), and per
+// 32-column group g the kernel forms smax = max|source|, amax = max|deq|,
+// limit = max(fp64(smax) * 32, 2^-126) and ratio = fp64(amax) / limit.
+// Results go to `stats` (zeroed by the caller) with one atomic per block:
+//   u64[0] non-finite dequantized values, u64[1] groups with amax > limit,
+//   u64[2] max ratio (bits of a non-negative fp64; NaN ratios skipped),
+//   u64[3] max |source| (bits of a non-negative fp32), u64[4] max |deq|.
+// The grid is capped (grid-stride loop), so the atomics stay few.
+constexpr int kAuditBlocks = 2048;
+
+__device__ inline float nanless_max(float a, float b) { return b > a ? b : a; }
+
+struct AuditAcc {
+  unsigned long long nonfinite = 0, exceed = 0;
+  double rmax = 0.0;
+  float smax = 0.0f, amax = 0.0f;
+  // one group's maxima, held by its leading lane
+  __device__ void group(float gs, float ga) {
+    const double limit = fmax(static_cast<double>(gs) * 32.0, 0x1p-126);
+    const double r = static_cast<double>(ga) / limit;
+    if (static_cast<double>(ga) > limit) ++exceed;
+    if (r == r) rmax = fmax(rmax, r);
+    smax = nanless_max(smax, gs);
+    amax = nanless_max(amax, ga);
+  }
+  // wave, then workgroup reduction; one atomic per block and field
+  __device__ void flush(unsigned long long* stats) {
+    __shared__ unsigned long long s_cnt[2][kThreads / 64];
+    __shared__ double s_r[kThreads / 64];
+    __shared__ float s_m[2][kThreads / 64];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      nonfinite += __shfl_xor(nonfinite, o);
+      exceed += __shfl_xor(exceed, o);
+      rmax = fmax(rmax, __shfl_xor(rmax, o));
+      smax = nanless_max(smax, __shfl_xor(smax, o));
+      amax = nanless_max(amax, __shfl_xor(amax, o));
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      s_cnt[0][w] = nonfinite, s_cnt[1][w] = exceed, s_r[w] = rmax;
+      s_m[0][w] = smax, s_m[1][w] = amax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int k = 1; k < kThreads / 64; ++k) {
+        s_cnt[0][0] += s_cnt[0][k], s_cnt[1][0] += s_cnt[1][k];
+        s_r[0] = fmax(s_r[0], s_r[k]);
+        s_m[0][0] = nanless_max(s_m[0][0], s_m[0][k]);
+        s_m[1][0] = nanless_max(s_m[1][0], s_m[1][k]);
+      }
+      if (s_cnt[0][0]) atomicAdd(&stats[0], s_cnt[0][0]);
+      if (s_cnt[1][0]) atomicAdd(&stats[1], s_cnt[1][0]);
+      atomicMax(&stats[2], static_cast<unsigned long long>(__double_as_longlong(s_r[0])));
+      atomicMax(&stats[3], static_cast<unsigned long long>(__float_as_uint(s_m[0][0])));
+      atomicMax(&stats[4], static_cast<unsigned long long>(__float_as_uint(s_m[1][0])));
+    }
+  }
+};
+
+__device__ inline float audit_deq(uint32_t c, float sc, float bias, int mode) {
+  if (mode == kAffine) return static_cast<float>(c) * sc + bias;
+  return ((mode == kMxfp4) ? e2m1_value(c & 15u) : e4m3_value(c)) * sc;
+}
+
+// One element per lane (any alignment, any affine group size); the 32 lanes
+// of a half-wave hold one group together (n and the stride are multiples
+// of 32).
+__global__ void __launch_bounds__(kThreads)
+    range_audit_kernel(const void* __restrict__ src, int src_dtype, const uint8_t* __restrict__ q,
+                       const void* __restrict__ scales, const void* __restrict__ biases,
+                       int storage, int mode, int64_t group_size, int64_t n,
+                       unsigned long long* __restrict__ stats) {
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  AuditAcc acc;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i - (lane & 31) < n;
+       i += stride) {
+    const float sv = fabsf(load_any(src, i, src_dtype));
+    float sc, bias = 0.0f;
+    if (mode == kAffine) {
+      const int64_t g = i / group_size;
+      sc = load_storage(scales, g, storage);
+      bias = load_storage(biases, g, storage);
+    } else {
+      sc = scale_from_byte(static_cast<const uint8_t*>(scales)[i / kMxGroup]);
+    }
+    const float v = audit_deq(q[i], sc, bias, mode);
+    if (!isfinite(v)) ++acc.nonfinite;
+    float gs = sv, ga = fabsf(v);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) {
+      gs = nanless_max(gs, __shfl_xor(gs, o));
+      ga = nanless_max(ga, __shfl_xor(ga, o));
+    }
+    if ((lane & 31) == 0) acc.group(gs, ga);
+  }
+  acc.flush(stats);
+}
+
+// Eight elements per lane from 16-byte-aligned rows: 16 (bf16 / f16) or 32
+// (f32) bytes of source and 8 code bytes per load; four lanes hold one
+// 32-column group (n8 = n / 8 and the stride are multiples of 4). The
+// affine group size is a multiple of 8, so a lane's eight values share one
+// scale. Each lane issues the loads of kAuditUnroll grid-stride units
+// before it evaluates any of them (2 and 4 measured no faster than 1; 4
+// needs 102 VGPRs). For MXFP4 (MX4 = true) a lane needs no per-element
+// dequantization: every value of a group is e2m1(c) * sc with one positive
+// power-of-two scale, so max|deq| = e2m1(max(c & 7)) * sc (0 when every
+// code is 0), and the values are non-finite exactly when sc is inf (E8M0
+// byte 255). max|source| is taken on the bit patterns with the sign cleared
+// (monotonic in |x|; NaN patterns count as 0, as the float path's compare
+// skips NaN).
+constexpr int kAuditUnroll = 1;
+
+template <int SD>
+__device__ inline float src_absmax(const uint4& a, const uint4& b) {
+  if constexpr (SD == kF32) {
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t v = w[k] & 0x7fffffffu;
+      m = max(m, v > 0x7f800000u ? 0u : v);
+    }
+    return __uint_as_float(m);
+  } else {
+    constexpr uint32_t kInf = (SD == kBF16) ? 0x7f80u : 0x7c00u;
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
+      m = max(m, max(lo > kInf ? 0u : lo, hi > kInf ? 0u : hi));
+    }
+    return (SD == kBF16) ? __uint_as_float(m << 16) : f16_to_f32(static_cast<uint16_t>(m));
+  }
+}
+
+template <int SD, bool MX4>
+__global__ void __launch_bounds__(kThreads)
+    range_audit_vec_kernel(const void* __restrict__ src, const uint8_t* __restrict__ q,
+                           const void* __restrict__ scales, const void* __restrict__ biases,
+                           int storage, int mode, int64_t group_size, int64_t n8,
+                           unsigned long long* __restrict__ stats) {
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  AuditAcc acc;
+  for (int64_t t0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t0 - (lane & 3) < n8;
+       t0 += stride * kAuditUnroll) {
+    uint4 ra[kAuditUnroll], rb[kAuditUnroll];
+    uint2 rc[kAuditUnroll];
+    float sc[kAuditUnroll], bias[kAuditUnroll];
+    bool on[kAuditUnroll];
+#pragma unroll
+    for (int u = 0; u < kAuditUnroll; ++u) {
+      const int64_t t = t0 + u * stride;
+      on[u] = t - (lane & 3) < n8;  // the same in the group's four lanes
+      bias[u] = 0.0f;
+      if (on[u]) {
+        if constexpr (SD == kF32) {
+          ra[u] = reinterpret_cast<const uint4*>(src)[2 * t];
+          rb[u] = reinterpret_cast<const uint4*>(src)[2 * t + 1];
+        } else {
+          ra[u] = reinterpret_cast<const uint4*>(src)[t];
+        }
+        rc[u] = reinterpret_cast<const uint2*>(q)[t];
+        if (mode == kAffine) {
+          const int64_t g = (8 * t) / group_size;
+          sc[u] = load_storage(scales, g, storage);
+          bias[u] = load_storage(biases, g, storage);
+        } else {
+          sc[u] = scale_from_byte(static_cast<const uint8_t*>(scales)[t >> 2]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAuditUnroll; ++u) {
+      if (!on[u]) continue;
+      if constexpr (MX4) {
+        float gs = src_absmax<SD>(ra[u], rb[u]);
+        const uint32_t x = rc[u].x & 0x07070707u, y = rc[u].y & 0x07070707u;
+        uint32_t mc = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mc = max(mc, max((x >> (8 * k)) & 7u, (y >> (8 * k)) & 7u));
+        float ga = mc ? e2m1_value(mc) * sc[u] : 0.0f;
+        if (isinf(sc[u])) acc.nonfinite += 8;
+#pragma unroll
+        for (int o = 2; o >= 1; o >>= 1) {
+          gs = nanless_max(gs, __shfl_xor(gs, o));
+          ga = nanless_max(ga, __shfl_xor(ga, o));
+        }
+        if ((lane & 3) == 0) acc.group(gs, ga);
+        continue;
+      }
+      float sv[8];
+      if constexpr (SD == kF32) {
+        sv[0] = __uint_as_float(ra[u].x), sv[1] = __uint_as_float(ra[u].y);
+        sv[2] = __uint_as_float(ra[u].z), sv[3] = __uint_as_float(ra[u].w);
+        sv[4] = __uint_as_float(rb[u].x), sv[5] = __uint_as_float(rb[u].y);
+        sv[6] = __uint_as_float(rb[u].z), sv[7] = __uint_as_float(rb[u].w);
+      } else {
+        const uint32_t w[4] = {ra[u].x, ra[u].y, ra[u].z, ra[u].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if constexpr (SD == kBF16) {
+            sv[2 * k] = __uint_as_float(w[k] << 16);
+            sv[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+          } else {
+            sv[2 * k] = f16_to_f32(static_cast<uint16_t>(w[k] & 0xffffu));
+            sv[2 * k + 1] = f16_to_f32(static_cast<uint16_t>(w[k] >> 16));
+          }
+        }
+      }
+      float gs = 0.0f, ga = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t c = ((k < 4 ? rc[u].x : rc[u].y) >> (8 * (k & 3))) & 0xffu;
+        const float v = audit_deq(c, sc[u], bias[u], mode);
+        if (!isfinite(v)) ++acc.nonfinite;
+        gs = nanless_max(gs, fabsf(sv[k]));
+        ga = nanless_max(ga, fabsf(v));
+      }
+#pragma unroll
+      for (int o = 2; o >= 1; o >>= 1) {
+        gs = nanless_max(gs, __shfl_xor(gs, o));
+        ga = nanless_max(ga, __shfl_xor(ga, o));
+      }
+      if ((lane & 3) == 0) acc.group(gs, ga);
+    }
+  }
+  acc.flush(stats);
+}
+
+template <bool MX4>
+void launch_audit_vec(int sd, unsigned blocks, hipStream_t st, const void* src, const uint8_t* q,
+                      const void* scales, const void* biases, int storage, int mode,
+                      int64_t group_size, int64_t n8, unsigned long long* stats) {
+  if (sd == kF32)
+    range_audit_vec_kernel<kF32, MX4><<<blocks, kThreads, 0, st>>>(src, q, scales, biases, storage,
+                                                                   mode, group_size, n8, stats);
+  else if (sd == kBF16)
+    range_audit_vec_kernel<kBF16, MX4><<<blocks, kThreads, 0, st>>>(src, q, scales, biases, storage,
+                                                                    mode, group_size, n8, stats);
+  else
+    range_audit_vec_kernel<kF16, MX4><<<blocks, kThreads, 0, st>>>(src, q, scales, biases, storage,
+                                                                   mode, group_size, n8, stats);
+}
+
 }  // namespace
 }  // namespace mgq
 
@@ -434,4 +686,46 @@ extern "C" int mgq_rtn_quantize_affine(const void* W, int w_dtype, int64_t rows,
       static_cast<const float*>(W), n_groups, group_size, static_cast<float>((1 << bits) - 1),
       storage_dtype, sh, q, s_store, b_store, dq);
   return check_launch("rtn_quantize");
+}
+
+extern "C" int mgq_range_audit(const void* source, int source_dtype, const uint8_t* q,
+                               const void* scales, const void* biases, int storage_dtype,
+                               int mode, int64_t rows, int64_t cols, int64_t group_size,
+                               unsigned long long* stats, void* stream) {
+  clear_error();
+  if (int rc = check_dtype(source_dtype, "range_audit")) return rc;
+  MGQ_REQUIRE(mode == kAffine || mode == kMxfp4 || mode == kMxfp8, MGQ_ERR_VALUE,
+              "unsupported mode %d", mode);
+  MGQ_REQUIRE(rows >= 0 && cols >= 0, MGQ_ERR_SHAPE, "bad shape");
+  MGQ_REQUIRE(cols % kMxGroup == 0, MGQ_ERR_SHAPE, "columns %lld not divisible by %d",
+              (long long)cols, kMxGroup);
+  if (mode == kAffine) {
+    if (int rc = check_dtype(storage_dtype, "range_audit")) return rc;
+    MGQ_REQUIRE(group_size >= 1 && cols % group_size == 0, MGQ_ERR_SHAPE,
+                "columns %lld not divisible by group %lld", (long long)cols,
+                (long long)group_size);
+    MGQ_REQUIRE(biases != nullptr, MGQ_ERR_VALUE, "affine artifacts need biases");
+  } else {
+    MGQ_REQUIRE(group_size == kMxGroup, MGQ_ERR_VALUE, "mxfp requires group size %d", kMxGroup);
+  }
+  MGQ_REQUIRE(stats != nullptr, MGQ_ERR_VALUE, "stats required");
+  const int64_t n = rows * cols;
+  if (n == 0) return MGQ_OK;
+  hipStream_t st = as_stream(stream);
+  const bool vec = ((reinterpret_cast<uintptr_t>(source) | reinterpret_cast<uintptr_t>(q)) & 15u) == 0 &&
+                   (mode != kAffine || group_size % 8 == 0);
+  const int64_t units = vec ? n / 8 : n;
+  int64_t nb = (units + kThreads - 1) / kThreads;
+  if (nb > kAuditBlocks) nb = kAuditBlocks;
+  const unsigned blocks = static_cast<unsigned>(nb);
+  if (!vec)
+    range_audit_kernel<<<blocks, kThreads, 0, st>>>(source, source_dtype, q, scales, biases,
+                                                    storage_dtype, mode, group_size, n, stats);
+  else if (mode == kMxfp4)
+    launch_audit_vec<true>(source_dtype, blocks, st, source, q, scales, biases, storage_dtype,
+                           mode, group_size, units, stats);
+  else
+    launch_audit_vec<false>(source_dtype, blocks, st, source, q, scales, biases, storage_dtype,
+                            mode, group_size, units, stats);
+  return check_launch("range_audit");
 }

@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "mgq_dequantize_mxfp": [_VP, _VP, _I64, _INT, _VP, _VP],
     "mgq_rtn_quantize_mxfp": [_VP, _INT, _I64, _I64, _INT, _VP, _VP, _VP, _VP],
     "mgq_dequantize_affine": [_VP, _VP, _VP, _INT, _I64, _I64, _VP, _VP],
+    "mgq_range_audit": [_VP, _INT, _VP, _VP, _VP, _INT, _INT, _I64, _I64, _I64, _VP, _VP],
     "mgq_choose_qparams": [_VP, _I64, _I64, _INT, _INT, _INT, _INT, _F64, _VP, _VP, _VP, _VP, _VP],
     "mgq_quantize_with_params": [_VP, _VP, _VP, _I64, _I64, _INT, _VP, _VP, _VP],
     "mgq_rtn_quantize_affine": [_VP, _INT, _I64, _I64, _INT, _INT, _INT, _INT, _VP, _VP, _VP, _VP, _VP],
