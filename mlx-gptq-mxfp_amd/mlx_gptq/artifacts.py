@@ -59,7 +59,7 @@ def unpack_nibbles(p: torch.Tensor) -> torch.Tensor:
 def _to_host(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
     """Contiguous CPU copies; device tensors go through pinned buffers with
     one synchronisation for the whole set."""
-    out, pending = {}, False
+    out, pending, seen = {}, False, set()
     for k, t in tensors.items():
         t = t.detach()
         if t.is_cuda:
@@ -68,7 +68,12 @@ def _to_host(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
             out[k] = h
             pending = True
         else:
-            out[k] = t.contiguous()
+            t = t.contiguous()
+            # safetensors refuses two names over one buffer
+            if t.numel() and t.untyped_storage().data_ptr() in seen:
+                t = t.clone()
+            seen.add(t.untyped_storage().data_ptr())
+            out[k] = t
     if pending:
         torch.cuda.synchronize()
     return out
