@@ -210,6 +210,7 @@ class RoutedStash:
         self.chunks: list[torch.Tensor] = []
         self._experts: list[torch.Tensor] = []  # int32 expert id per assignment
         self._rows: list[torch.Tensor] = []  # int32 row of the buffer per assignment
+        self._pending: list[tuple[int, torch.Tensor]] = []  # (first row, top-k ids [T, k])
         self.rows = 0  # rows stored
         self._plan = None
 
@@ -236,13 +237,29 @@ class RoutedStash:
         ti = top_k_index.detach()
         if ti.dtype.is_floating_point or ti.numel() % max(T, 1) != 0:
             raise ValueError(f"stash {self.name}: top_k_index must hold k integer ids per row")
-        ti = ti.reshape(T, -1).to(device=rows.device)
-        k = ti.shape[1]
+        # the (expert, row) lists are built by plan(), for all batches at once
+        self._pending.append((base, ti.reshape(T, -1).to(device=rows.device, copy=True)))
+
+    def _assign(self, ti: torch.Tensor, base: int):
+        T, k = ti.shape
         e = ti.reshape(-1).to(torch.int64)
         e = torch.where((e >= 0) & (e < self.num_experts), e, self.num_experts).to(torch.int32)
-        r = (torch.arange(T, device=rows.device, dtype=torch.int32) + base).repeat_interleave(k)
+        r = (torch.arange(T, device=ti.device, dtype=torch.int32) + base).repeat_interleave(k)
         self._experts.append(e)
         self._rows.append(r)
+
+    def _materialize(self):
+        p = self._pending
+        if not p:
+            return
+        same_k = len({ti.shape[1] for _, ti in p}) == 1
+        back_to_back = all(p[i + 1][0] == p[i][0] + p[i][1].shape[0] for i in range(len(p) - 1))
+        if same_k and back_to_back:
+            self._assign(p[0][1] if len(p) == 1 else torch.cat([ti for _, ti in p]), p[0][0])
+        else:
+            for base, ti in p:
+                self._assign(ti, base)
+        self._pending = []
 
     def add_rows(self, expert: int, x: torch.Tensor):
         """Rows x that belong to `expert` alone."""
@@ -254,7 +271,8 @@ class RoutedStash:
         self._rows.append(torch.arange(base, base + n, dtype=torch.int32, device=rows.device))
 
     def nbytes(self) -> int:
-        return sum(c.numel() * 2 for c in self.chunks) + sum(r.numel() * 8 for r in self._rows)
+        return (sum(c.numel() * 2 for c in self.chunks) + sum(r.numel() * 8 for r in self._rows)
+                + sum(ti.numel() * ti.element_size() for _, ti in self._pending))
 
     def plan(self) -> tuple[torch.Tensor, np.ndarray, torch.Tensor]:
         """(X, offsets, row_index): X bf16 [rows, C], the stored rows;
@@ -266,6 +284,7 @@ class RoutedStash:
                 raise RuntimeError(f"stash {self.name}: nothing captured")
             X = self.chunks[0] if len(self.chunks) == 1 else torch.cat(self.chunks)
             self.chunks = [X]
+            self._materialize()
             e = torch.cat(self._experts)
             r = torch.cat(self._rows)
             e_sorted, order = torch.sort(e, stable=True)
@@ -327,6 +346,7 @@ class RoutedStash:
         self.chunks.clear()
         self._experts.clear()
         self._rows.clear()
+        self._pending.clear()
         self.rows = 0
         self._plan = None
 
