@@ -378,6 +378,8 @@ class ExpertCapture:
         self._input_key: dict[str, str] = {}  # module name -> shared input stash key
         self._ptr: dict[int, tuple[str, int, str]] = {}  # slice ptr -> (key, expert, module)
         self._routed: dict[str, bool] = {}
+        self._samples: dict[str, Stash] = {}  # module -> sampled block inputs (backfill source)
+        self.fallback_experts: dict[str, str] = {}
         self._hooks = []
         self._mode = None
         self.skipped: list[str] = []
@@ -394,6 +396,7 @@ class ExpertCapture:
                     ik = self._input_key.setdefault(name, key)
                     if ik not in self.stashes:
                         self.stashes[ik] = RoutedStash(f"{name}::inputs", C, E)
+                        self._samples[name] = Stash(f"{name}::all_inputs", C)
                     self.stashes[key] = self.stashes[ik]
                 else:
                     self.stashes[key] = RoutedStash(key, C, E)
@@ -422,6 +425,10 @@ class ExpertCapture:
             self._routed[name] = bool(ok)
             if ok:
                 self.stashes[ik].add_routed(x, ti)
+            if ik is not None and isinstance(x, torch.Tensor):
+                # 64 evenly spaced rows per batch: the activation-aware
+                # fallback for experts the router never picks (capture.py:177-184)
+                self._samples[name].add_sampled(x, 64)
         return hook
 
     class _Mode(TorchFunctionMode):
@@ -485,6 +492,51 @@ class ExpertCapture:
                     "load the model with experts_implementation='eager'."
                 )
 
+    @torch.no_grad()
+    def backfill_unrouted_experts(self) -> dict[str, list[int]]:
+        """Rows for experts that got none (capture.py:250-318): the block's
+        sampled inputs for the input parameters, and for ``down_proj`` the
+        activations SiLU(gate) * up of those rows under that expert's own
+        weights. Returns module -> backfilled experts; the affected
+        ``{key}::e{e}`` names are listed in ``fallback_experts``."""
+        out: dict[str, list[int]] = {}
+        for name, ik in self._input_key.items():
+            src = self._samples.get(name)
+            if src is None or src.tokens == 0:
+                continue
+            st = self.stashes[ik]
+            counts = st.token_counts()
+            missing = [e for e in range(st.num_experts) if counts[e] == 0]
+            if not missing:
+                continue
+            params = {pn: p for (mn, pn, p) in self.params.values() if mn == name}
+            in_keys = [k for k, (mn, pn, _) in self.params.items() if mn == name and pn in _INPUT_PARAMS]
+            dk = next((k for k, (mn, pn, _) in self.params.items() if mn == name and pn == "down_proj"), None)
+            for e in missing:
+                for chunk in src.chunks:
+                    st.add_rows(e, chunk)
+                for k in in_keys:
+                    self.fallback_experts[f"{k}::e{e}"] = "all_expert_inputs"
+                if dk is None:
+                    continue
+                down = self.stashes[dk]
+                before = down.rows
+                for chunk in src.chunks:
+                    if "gate_up_proj" in params:
+                        w = params["gate_up_proj"][e]
+                        gate, up = F.linear(chunk.to(w.device, w.dtype), w).chunk(2, dim=-1)
+                        down.add_rows(e, F.silu(gate) * up)
+                    elif "gate_proj" in params and "up_proj" in params:
+                        wg, wu = params["gate_proj"][e], params["up_proj"][e]
+                        x = chunk.to(wg.device, wg.dtype)
+                        down.add_rows(e, F.silu(F.linear(x, wg)) * F.linear(x, wu))
+                if down.rows > before:
+                    self.fallback_experts[f"{dk}::e{e}"] = "all_expert_inputs"
+            out[name] = missing
+        return out
+
     def drop_all(self):
         for st in self.stashes.values():
+            st.clear()
+        for st in self._samples.values():
             st.clear()

@@ -177,6 +177,42 @@ def test_fallback_without_top_k_records_slice_inputs():
             assert torch.equal(st.expert_rows(e), _recorded(rec, pname, e, C))
 
 
+def test_backfill_unrouted_experts():
+    blk = _block(E=8, k=2)
+    gate_fwd = blk.gate.forward
+
+    def never_seven(h):  # the router never picks expert 7
+        logits, _, _ = gate_fwd(h)
+        masked = logits.clone()
+        masked[:, 7] = -float("inf")
+        probs = torch.softmax(masked, dim=-1, dtype=torch.float)
+        vals, idx = torch.topk(probs, 2, dim=-1)
+        return logits, (vals / vals.sum(-1, keepdim=True)).to(logits.dtype), idx
+
+    blk.gate.forward = never_seven
+    cap = capture.ExpertCapture(blk)
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(1, 100, 64, generator=g), torch.randn(2, 10, 64, generator=g)]
+    with torch.no_grad(), cap:
+        for x in xs:
+            blk(x)
+    gu, dn = cap.stashes["experts.gate_up_proj"], cap.stashes["experts.down_proj"]
+    assert gu.token_counts()[7] == 0 and dn.token_counts()[7] == 0
+    assert cap.backfill_unrouted_experts() == {"experts": [7]}
+    # the sample: 64 evenly spaced rows of a batch with more than 64 (capture.py:52-63)
+    rows = [x.reshape(-1, 64) for x in xs]
+    sample = torch.cat([rows[0][torch.linspace(0, 99, 64).long()], rows[1]]).to(torch.bfloat16)
+    assert torch.equal(gu.expert_rows(7), sample)
+    # down inputs: the sample in the weights' dtype through expert 7's own
+    # gate/up projections (capture.py:300-306), stored as bf16
+    w = blk.experts.gate_up_proj[7].detach()
+    gate, up = F.linear(sample.to(w.dtype), w).chunk(2, dim=-1)
+    assert torch.equal(dn.expert_rows(7), (F.silu(gate) * up).to(torch.bfloat16))
+    assert cap.fallback_experts == {"experts.gate_up_proj::e7": "all_expert_inputs",
+                                    "experts.down_proj::e7": "all_expert_inputs"}
+    assert cap.backfill_unrouted_experts() == {}
+
+
 def test_group_size_skip_and_no_capture_error():
     blk = _block(hidden=48, inter=32)
     cap = capture.ExpertCapture(blk, group_size=32)
