@@ -1,20 +1,29 @@
-"""Calibration artifact store (artifacts.py API) on MI355X.
+"""Calibration artifact store (the reference's artifacts.py API) on MI355X.
 
-Directory layout, the same as the reference's (artifacts.py:1-15) so that
-either side's reader takes either side's output:
+On-disk format, shared with the reference (artifacts.py:1-15) so that either
+side reads the other's output:
 
     calib_dir/
-      manifest.json            header + "tensors" (per-tensor metadata) + "layers_done"
+      manifest.json            run header + "tensors" {name: info} + "layers_done" [int]
       layer_0000.safetensors   {name}.q / {name}.scales / optional {name}.biases
       ...
 
-4-bit codes are stored nibble-packed, two per byte, low nibble first
-(``"q_packed": "nibble"``), other widths raw. ``ArtifactWriter.write_layer``
-takes the solver's device tensors as they are: the 4-bit codes are packed on
-the device (csrc/pack.hip), every tensor of the layer is copied into pinned
-host memory with one synchronisation, and the layer file is written under a
-temporary name and renamed. The manifest is rewritten atomically after each
-layer, as the reference does.
+``info`` carries the solver's metadata plus three storage fields:
+``"q_packed"`` ("nibble": 4-bit codes two per byte, low nibble first;
+"raw": one code per byte), ``"has_biases"`` and ``"file"``.
+
+Design:
+
+* ``_Manifest`` owns the JSON document: resume validation against the run
+  header, and atomic replacement (temporary file + rename) on every save.
+* Codes are encoded by a per-bit-width codec (``_CODECS``); 4-bit packing
+  runs on the HIP device (``mgq_pack_nibbles``), so ``write_layer`` takes the
+  solver's device tensors as they are. The layer's tensors are staged into
+  pinned host buffers and synchronised once, and the layer file is written
+  under a temporary name and renamed.
+* ``ArtifactReader`` opens layer files lazily with ``safe_open`` and reads
+  only the tensors asked for (a few handles kept open, least recently used
+  closed first) instead of loading whole layer files.
 """
 
 from __future__ import annotations
@@ -22,163 +31,190 @@ from __future__ import annotations
 import json
 import os
 import tempfile
+from collections import OrderedDict
 
 import torch
 
 from . import _native as nat
 
-_STR_TO_DTYPE = {"bfloat16": torch.bfloat16, "float16": torch.float16}
-_RESUME_KEYS = ("mode", "bits", "group_size", "storage_dtype")
+_STORAGE_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16}
+
+# header fields a resumed run must agree on; the message is the reference's
+_RESUME_FIELDS = ("mode", "bits", "group_size", "storage_dtype")
+
+
+def _nibble_kernel(name: str, src: torch.Tensor, out_last: int) -> torch.Tensor:
+    """Run one of the byte <-> nibble kernels over the last axis of `src`."""
+    dev = nat.device_for(src)
+    x = nat.on_device(src.to(torch.uint8), dev)
+    *lead, n = src.shape
+    rows = nat.numel_groups(tuple(lead))
+    out = torch.empty((*lead, out_last), dtype=torch.uint8, device=dev)
+    if rows and n:
+        nat.call(name, x.data_ptr(), rows, n, out.data_ptr(), nat.stream_of(dev))
+    return out.to(src.device)
 
 
 def pack_nibbles(q: torch.Tensor) -> torch.Tensor:
-    """uint8 [..., C] -> uint8 [..., C/2] with byte = q[2k] | q[2k+1] << 4 (artifacts.py:30-32)."""
+    """uint8 [..., C] -> uint8 [..., C/2], byte k = q[2k] | q[2k+1] << 4
+    (artifacts.py:30-32)."""
     assert q.dtype == torch.uint8 and q.shape[-1] % 2 == 0
-    dev = nat.device_for(q)
-    x = nat.on_device(q, dev)
-    *lead, C = q.shape
-    rows = nat.numel_groups(tuple(lead))
-    out = torch.empty((*lead, C // 2), dtype=torch.uint8, device=dev)
-    if rows and C:
-        nat.call("mgq_pack_nibbles", x.data_ptr(), rows, C, out.data_ptr(), nat.stream_of(dev))
-    return out.to(q.device)
+    return _nibble_kernel("mgq_pack_nibbles", q, q.shape[-1] // 2)
 
 
 def unpack_nibbles(p: torch.Tensor) -> torch.Tensor:
     """uint8 [..., P] -> uint8 [..., 2P], low nibble first (artifacts.py:35-39)."""
-    dev = nat.device_for(p)
-    x = nat.on_device(p.to(torch.uint8), dev)
-    *lead, P = p.shape
-    rows = nat.numel_groups(tuple(lead))
-    out = torch.empty((*lead, 2 * P), dtype=torch.uint8, device=dev)
-    if rows and P:
-        nat.call("mgq_unpack_nibbles", x.data_ptr(), rows, P, out.data_ptr(), nat.stream_of(dev))
-    return out.to(p.device)
+    return _nibble_kernel("mgq_unpack_nibbles", p, 2 * p.shape[-1])
 
 
-def _to_host(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
-    """Contiguous CPU copies; device tensors go through pinned buffers with
-    one synchronisation for the whole set."""
-    out, pending, seen = {}, False, set()
-    for k, t in tensors.items():
+# bits -> (q_packed tag, encode, decode); widths not listed are stored raw
+_CODECS = {4: ("nibble", pack_nibbles, unpack_nibbles)}
+_RAW = ("raw", lambda q: q, lambda q: q)
+_DECODERS = {tag: dec for tag, _, dec in (*_CODECS.values(), _RAW)}
+
+
+class _Manifest:
+    """manifest.json of one artifact directory."""
+
+    def __init__(self, directory: str, header: dict | None):
+        self.path = os.path.join(directory, "manifest.json")
+        self.dir = directory
+        if os.path.exists(self.path):
+            with open(self.path) as f:
+                self.doc = json.load(f)
+            for key in _RESUME_FIELDS:
+                if header is not None and key in header and self.doc.get(key) != header[key]:
+                    raise RuntimeError(
+                        f"resume mismatch: manifest has {key}={self.doc.get(key)}, "
+                        f"run has {header[key]}"
+                    )
+        elif header is None:
+            raise FileNotFoundError(self.path)
+        else:
+            self.doc = {**header, "tensors": {}, "layers_done": []}
+
+    def record_layer(self, layer_idx: int, infos: dict) -> None:
+        self.doc["tensors"].update(infos)
+        self.doc["layers_done"].append(layer_idx)
+        self.save()
+
+    def save(self) -> None:
+        fd, tmp = tempfile.mkstemp(dir=self.dir, suffix=".json.tmp")
+        with os.fdopen(fd, "w") as f:
+            json.dump(self.doc, f)
+        os.replace(tmp, self.path)
+
+
+def _stage_to_host(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
+    """Contiguous host copies: device tensors through pinned buffers with one
+    synchronisation for the whole set; host tensors that share storage are
+    cloned (safetensors refuses aliases)."""
+    staged, on_device, storages = {}, False, set()
+    for key, t in tensors.items():
         t = t.detach()
         if t.is_cuda:
-            h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-            h.copy_(t.contiguous(), non_blocking=True)
-            out[k] = h
-            pending = True
+            host = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+            host.copy_(t.contiguous(), non_blocking=True)
+            on_device = True
         else:
-            t = t.contiguous()
-            # safetensors refuses two names over one buffer
-            if t.numel() and t.untyped_storage().data_ptr() in seen:
-                t = t.clone()
-            seen.add(t.untyped_storage().data_ptr())
-            out[k] = t
-    if pending:
+            host = t.contiguous()
+            sid = host.untyped_storage().data_ptr()
+            if host.numel() and sid in storages:
+                host = host.clone()
+            storages.add(host.untyped_storage().data_ptr())
+        staged[key] = host
+    if on_device:
         torch.cuda.synchronize()
-    return out
+    return staged
+
+
+def _atomic_save(flat: dict[str, torch.Tensor], path: str) -> None:
+    from safetensors.torch import save_file
+
+    fd, tmp = tempfile.mkstemp(dir=os.path.dirname(path), suffix=".safetensors.tmp")
+    os.close(fd)
+    try:
+        save_file(flat, tmp)
+        os.replace(tmp, path)
+    except BaseException:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+        raise
 
 
 class ArtifactWriter:
-    """Stage-A artifact store (artifacts.py:42-102): same manifest keys,
-    resume check and file names."""
+    """Stage-A side of the store (artifacts.py:42-102)."""
 
     def __init__(self, out_dir: str, header: dict):
-        self.dir = out_dir
         os.makedirs(out_dir, exist_ok=True)
-        self.manifest_path = os.path.join(out_dir, "manifest.json")
-        if os.path.exists(self.manifest_path):
-            with open(self.manifest_path) as f:
-                self.manifest = json.load(f)
-            for k, v in header.items():
-                if k in _RESUME_KEYS and self.manifest.get(k) != v:
-                    raise RuntimeError(
-                        f"resume mismatch: manifest has {k}={self.manifest.get(k)}, run has {v}"
-                    )
-        else:
-            self.manifest = dict(header)
-            self.manifest["tensors"] = {}
-            self.manifest["layers_done"] = []
+        self.dir = out_dir
+        self._m = _Manifest(out_dir, header)
+        self.manifest_path = self._m.path
+
+    @property
+    def manifest(self) -> dict:
+        return self._m.doc
 
     def layer_done(self, layer_idx: int) -> bool:
-        return layer_idx in self.manifest["layers_done"]
+        return layer_idx in self._m.doc["layers_done"]
 
     def layer_file(self, layer_idx: int) -> str:
         return os.path.join(self.dir, f"layer_{layer_idx:04d}.safetensors")
 
     def write_layer(self, layer_idx: int, tensors: dict, meta: dict):
-        """tensors: name -> (q uint8 [out, in], scales, optional biases), on a
-        HIP device or the host; meta: name -> metadata with at least "bits"
-        (updated in place with "q_packed", "has_biases" and "file")."""
-        from safetensors.torch import save_file
-
-        fname = f"layer_{layer_idx:04d}.safetensors"
+        """tensors: name -> (q uint8 [out, in], scales, biases or None), on a
+        HIP device or the host; meta: name -> info with at least "bits",
+        completed in place with the storage fields."""
+        fname = os.path.basename(self.layer_file(layer_idx))
         flat = {}
-        for name, (q, s, b) in tensors.items():
-            if meta[name]["bits"] == 4:
-                q = pack_nibbles(q)
-                meta[name]["q_packed"] = "nibble"
-            else:
-                meta[name]["q_packed"] = "raw"
-            flat[f"{name}.q"] = q
-            flat[f"{name}.scales"] = s
-            meta[name]["has_biases"] = b is not None
-            if b is not None:
-                flat[f"{name}.biases"] = b
-            meta[name]["file"] = fname
-        flat = _to_host(flat)
-        fd, tmp = tempfile.mkstemp(dir=self.dir, suffix=".safetensors.tmp")
-        os.close(fd)
-        try:
-            save_file(flat, tmp)
-            os.replace(tmp, self.layer_file(layer_idx))
-        except BaseException:
-            if os.path.exists(tmp):
-                os.unlink(tmp)
-            raise
-        self.manifest["tensors"].update(meta)
-        self.manifest["layers_done"].append(layer_idx)
-        self._flush()
-
-    def _flush(self):
-        fd, tmp = tempfile.mkstemp(dir=self.dir, suffix=".json.tmp")
-        with os.fdopen(fd, "w") as f:
-            json.dump(self.manifest, f)
-        os.replace(tmp, self.manifest_path)
+        for name, (q, scales, biases) in tensors.items():
+            info = meta[name]
+            tag, encode, _ = _CODECS.get(info["bits"], _RAW)
+            flat[f"{name}.q"] = encode(q)
+            flat[f"{name}.scales"] = scales
+            if biases is not None:
+                flat[f"{name}.biases"] = biases
+            info.update(q_packed=tag, has_biases=biases is not None, file=fname)
+        _atomic_save(_stage_to_host(flat), self.layer_file(layer_idx))
+        self._m.record_layer(layer_idx, meta)
 
 
 class ArtifactReader:
-    """Stage-B reader (artifacts.py:105-139). ``get`` returns host tensors,
-    the 4-bit codes unpacked (on the HIP device)."""
+    """Stage-B side of the store (artifacts.py:105-126). ``get`` returns host
+    tensors; 4-bit codes are unpacked on the HIP device."""
 
-    def __init__(self, calib_dir: str):
+    def __init__(self, calib_dir: str, open_files: int = 4):
         self.dir = calib_dir
-        with open(os.path.join(calib_dir, "manifest.json")) as f:
-            self.manifest = json.load(f)
+        self.manifest = _Manifest(calib_dir, None).doc
         self.tensors = self.manifest["tensors"]
-        self._cache_file = None
-        self._cache = None
+        self._handles: OrderedDict[str, object] = OrderedDict()
+        self._open_files = max(1, int(open_files))
 
     @property
     def storage_dtype(self) -> torch.dtype:
-        return _STR_TO_DTYPE[self.manifest["storage_dtype"]]
+        return _STORAGE_DTYPES[self.manifest["storage_dtype"]]
 
     def has(self, name: str) -> bool:
         return name in self.tensors
 
-    def _load(self, fname: str) -> dict:
-        from safetensors.torch import load_file
+    def _file(self, fname: str):
+        from safetensors import safe_open
 
-        if self._cache_file != fname:
-            self._cache = load_file(os.path.join(self.dir, fname))
-            self._cache_file = fname
-        return self._cache
+        entry = self._handles.get(fname)
+        if entry is None:
+            h = safe_open(os.path.join(self.dir, fname), "pt")
+            entry = (h, frozenset(h.keys()))
+            self._handles[fname] = entry
+            while len(self._handles) > self._open_files:
+                self._handles.popitem(last=False)
+        else:
+            self._handles.move_to_end(fname)
+        return entry
 
     def get(self, name: str):
-        """(q uint8 [out, in], scales, optional biases, info)."""
+        """(q uint8 [out, in], scales, biases or None, info)."""
         info = self.tensors[name]
-        blob = self._load(info["file"])
-        q = blob[f"{name}.q"]
-        if info["q_packed"] == "nibble":
-            q = unpack_nibbles(q)
-        return q, blob[f"{name}.scales"], blob.get(f"{name}.biases"), info
+        f, keys = self._file(info["file"])
+        q = _DECODERS[info["q_packed"]](f.get_tensor(f"{name}.q"))
+        biases = f.get_tensor(f"{name}.biases") if f"{name}.biases" in keys else None
+        return q, f.get_tensor(f"{name}.scales"), biases, info

@@ -24,6 +24,9 @@ their expert id. Every expert's H then comes from one grouped launch.
 from __future__ import annotations
 
 import ctypes
+import logging
+import threading
+from dataclasses import dataclass, field
 from typing import Sequence
 
 import numpy as np
@@ -33,10 +36,26 @@ from torch.overrides import TorchFunctionMode
 
 from . import _native as nat
 
+log = logging.getLogger(__name__)
+
 # 3D expert parameter names of the transformers fused-expert layout
 # (capture.py:28); the first three take the MoE block's hidden states.
 FUSED_EXPERT_PARAMS = ("gate_up_proj", "gate_proj", "up_proj", "down_proj")
 _INPUT_PARAMS = ("gate_up_proj", "gate_proj", "up_proj")
+
+
+def _hip_device(device) -> torch.device:
+    """`device` as an indexed HIP device; Hessians are formed on HIP devices
+    only (there is no CPU path)."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "mlx_gptq (MI355X build) accumulates Hessians on HIP devices only "
+            f"(got device {dev})"
+        )
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return dev
 
 
 def _as_offsets(offsets) -> np.ndarray:
@@ -155,28 +174,33 @@ class Stash:
     def nbytes(self) -> int:
         return sum(c.numel() * 2 for c in self.chunks)
 
+    def rows_on(self, device) -> torch.Tensor:
+        """Every stored row as one contiguous bf16 [tokens, C] matrix on
+        `device`. The chunks are joined (and moved) once; the joined matrix
+        then replaces them, so later calls cost nothing."""
+        dev = torch.device(device)
+        if not self.chunks:
+            return torch.zeros(0, self.in_features, dtype=torch.bfloat16, device=dev)
+        if len(self.chunks) == 1 and self.chunks[0].device == dev:
+            return self.chunks[0]
+        X = torch.cat([c.to(dev, non_blocking=True) for c in self.chunks])
+        self.chunks = [X]
+        return X
+
     @torch.no_grad()
     def hessian(self, device, chunk_rows: int = 65536) -> torch.Tensor:
-        """H = X^T X in fp32 on `device` (capture.py:68-76)."""
-        dev = torch.device(device)
-        if dev.type != "cuda":
-            raise RuntimeError(
-                "mlx_gptq (MI355X build) accumulates Hessians on HIP devices only "
-                f"(got device {dev})"
-            )
-        C = self.in_features
-        H = torch.zeros(C, C, dtype=torch.float32, device=dev)
-        first = True
-        for c in self.chunks:
-            for i in range(0, c.shape[0], chunk_rows):
-                x = c[i : i + chunk_rows]
-                if x.device != dev:
-                    x = x.to(dev, non_blocking=True)
-                if x.shape[0] == 0:
-                    continue
-                hessian_xtx(x, out=H, accumulate=not first)
-                first = False
-        return H
+        """H = X^T X in fp32 on `device` (capture.py:68-76).
+
+        One SYRK launch over all stored rows: the kernel splits the token
+        range across workgroups itself, so there is no per-chunk launch or
+        read-modify-write of H. ``chunk_rows`` is accepted for signature
+        compatibility; in the reference it only sets the fp32 summation
+        blocks of its ``addmm`` loop."""
+        dev = _hip_device(device)
+        X = self.rows_on(dev)
+        if X.shape[0] == 0:
+            return torch.zeros(self.in_features, self.in_features, dtype=torch.float32, device=dev)
+        return hessian_xtx(X)
 
     def clear(self):
         self.chunks.clear()
@@ -201,18 +225,28 @@ class RoutedStash:
     Rows are rounded to bf16 as capture.py:49 does; the row order inside
     an expert differs from the eager loop's, which changes only the fp32
     summation order of H.
+
+    ``expert_hessian`` serves the reference's one-expert-at-a-time
+    ``stashes[key].hessian(device)`` calls (sequential.py:546-551): the
+    first call for expert e forms the Hessians of a whole span e, e+1, ...
+    (up to ``span_bytes`` of them) in one launch and hands the rest out
+    from a cache on the following calls.
     """
 
-    def __init__(self, name: str, in_features: int, num_experts: int):
+    def __init__(self, name: str, in_features: int, num_experts: int,
+                 span_bytes: int = 1 << 30):
         self.name = name
         self.in_features = int(in_features)
         self.num_experts = int(num_experts)
+        self.span_bytes = int(span_bytes)
         self.chunks: list[torch.Tensor] = []
         self._experts: list[torch.Tensor] = []  # int32 expert id per assignment
         self._rows: list[torch.Tensor] = []  # int32 row of the buffer per assignment
         self._pending: list[tuple[int, torch.Tensor]] = []  # (first row, top-k ids [T, k])
         self.rows = 0  # rows stored
         self._plan = None
+        self._hcache: dict[tuple[int, torch.device], torch.Tensor] = {}
+        self._lock = threading.RLock()
 
     def _append(self, x: torch.Tensor) -> tuple[torch.Tensor, int]:
         rows = x.detach().reshape(-1, x.shape[-1])
@@ -224,9 +258,11 @@ class RoutedStash:
         base = self.rows
         if base + rows.shape[0] > 2**31 - 1:
             raise RuntimeError(f"stash {self.name}: more than 2^31 - 1 rows")
-        self.chunks.append(rows.to(torch.bfloat16, copy=True).contiguous())
-        self.rows += rows.shape[0]
-        self._plan = None
+        if rows.shape[0]:
+            self.chunks.append(rows.to(torch.bfloat16, copy=True).contiguous())
+            self.rows += rows.shape[0]
+            self._plan = None
+            self._hcache.clear()
         return rows, base
 
     def add_routed(self, x: torch.Tensor, top_k_index: torch.Tensor):
@@ -237,6 +273,8 @@ class RoutedStash:
         ti = top_k_index.detach()
         if ti.dtype.is_floating_point or ti.numel() % max(T, 1) != 0:
             raise ValueError(f"stash {self.name}: top_k_index must hold k integer ids per row")
+        if T == 0:
+            return  # an empty batch routes nothing
         # the (expert, row) lists are built by plan(), for all batches at once
         self._pending.append((base, ti.reshape(T, -1).to(device=rows.device, copy=True)))
 
@@ -267,6 +305,8 @@ class RoutedStash:
             raise IndexError(f"stash {self.name}: expert {expert} outside [0, {self.num_experts})")
         rows, base = self._append(x)
         n = rows.shape[0]
+        if n == 0:
+            return
         self._experts.append(torch.full((n,), int(expert), dtype=torch.int32, device=rows.device))
         self._rows.append(torch.arange(base, base + n, dtype=torch.int32, device=rows.device))
 
@@ -285,6 +325,8 @@ class RoutedStash:
             X = self.chunks[0] if len(self.chunks) == 1 else torch.cat(self.chunks)
             self.chunks = [X]
             self._materialize()
+            if not self._experts:
+                raise RuntimeError(f"stash {self.name}: nothing captured")
             e = torch.cat(self._experts)
             r = torch.cat(self._rows)
             e_sorted, order = torch.sort(e, stable=True)
@@ -318,37 +360,68 @@ class RoutedStash:
         if experts.step != 1 or not 0 <= experts.start <= experts.stop <= E:
             raise ValueError(f"experts must be a contiguous span inside [0, {E})")
         C = self.in_features
-        if not self.chunks:
-            dev = torch.device(device) if device is not None else None
-            if dev is None or dev.type != "cuda":
-                raise RuntimeError("mlx_gptq (MI355X build) accumulates Hessians on HIP devices only")
-            return torch.zeros(len(experts), C, C, dtype=torch.float32, device=dev)
-        X, off, ri = self.plan()
-        if device is not None:
-            dev = torch.device(device)
-            if dev.type != "cuda":
-                raise RuntimeError(
-                    "mlx_gptq (MI355X build) accumulates Hessians on HIP devices only "
-                    f"(got device {dev})"
-                )
-            if X.device != dev:
-                X, ri = X.to(dev), ri.to(dev)
-                self.chunks, self._rows = [X], [ri]
-                self._plan = (X, off, ri)
+        with self._lock:
+            if not self.chunks:
+                dev = _hip_device("cuda" if device is None else device)
+                H = torch.zeros(len(experts), C, C, dtype=torch.float32, device=dev)
+                if out is not None:
+                    out.copy_(H)
+                    return out
+                return H
+            X, off, ri = self.plan()
+            if device is not None:
+                dev = _hip_device(device)
+                if X.device != dev:
+                    X, ri = X.to(dev), ri.to(dev)
+                    self.chunks, self._rows = [X], [ri]
+                    self._plan = (X, off, ri)
         return grouped_hessian(X, off[experts.start : experts.stop + 1], ri, out=out,
                                validate=False)
+
+    def expert_hessian(self, expert: int, device=None) -> torch.Tensor:
+        """One expert's H (fp32 [C, C]) for a caller that asks expert by
+        expert. A miss forms the Hessians of experts expert..expert+n-1
+        (n such that they fit in ``span_bytes``) in one grouped launch and
+        keeps the others for the following calls; each cached H is handed
+        out once."""
+        e = int(expert)
+        if not 0 <= e < self.num_experts:
+            raise IndexError(f"stash {self.name}: expert {e} outside [0, {self.num_experts})")
+        with self._lock:
+            dev = _hip_device("cuda" if device is None else device)
+            H = self._hcache.pop((e, dev), None)
+            if H is not None:
+                return H
+            C = self.in_features
+            n = max(1, min(self.num_experts - e, self.span_bytes // max(C * C * 4, 1)))
+            Hs = self.hessians(dev, range(e, e + n))
+            for i in range(1, n):
+                self._hcache[(e + i, dev)] = Hs[i]
+            return Hs[0]
 
     def hessian(self, expert: int, device=None) -> torch.Tensor:
         """One expert's H (fp32 [C, C]), the per-expert Stash.hessian."""
         return self.hessians(device, range(int(expert), int(expert) + 1))[0]
 
+    def drop_expert(self, expert: int):
+        """Forget expert `expert`'s rows (the per-expert Stash.clear)."""
+        e = int(expert)
+        with self._lock:
+            self._materialize()
+            for ids in self._experts:  # its assignments go to the ignored id E
+                ids.masked_fill_(ids == e, self.num_experts)
+            self._plan = None
+            self._hcache.clear()
+
     def clear(self):
-        self.chunks.clear()
-        self._experts.clear()
-        self._rows.clear()
-        self._pending.clear()
-        self.rows = 0
-        self._plan = None
+        with self._lock:
+            self.chunks.clear()
+            self._experts.clear()
+            self._rows.clear()
+            self._pending.clear()
+            self.rows = 0
+            self._plan = None
+            self._hcache.clear()
 
 
 class ExpertCapture:
@@ -379,6 +452,10 @@ class ExpertCapture:
         self._ptr: dict[int, tuple[str, int, str]] = {}  # slice ptr -> (key, expert, module)
         self._routed: dict[str, bool] = {}
         self._samples: dict[str, Stash] = {}  # module -> sampled block inputs (backfill source)
+        # module -> {expert: the input tensor last stored for it in the current
+        # call}: separate gate_proj / up_proj slices see the same tensor and
+        # share one stash, so the second F.linear must not store it again
+        self._last_in: dict[str, dict[int, torch.Tensor]] = {}
         self.fallback_experts: dict[str, str] = {}
         self._hooks = []
         self._mode = None
@@ -390,7 +467,9 @@ class ExpertCapture:
                 key = f"{name}.{pname}" if name else pname
                 E, C = p.shape[0], p.shape[-1]
                 if group_size and C % group_size != 0:
-                    self.skipped.append(key)  # capture.py:141-146
+                    log.warning("skipping fused %s.%s: in dim %d not divisible by group %d",
+                                name, pname, C, group_size)
+                    self.skipped.append(key)
                     continue
                 if pname in _INPUT_PARAMS:
                     ik = self._input_key.setdefault(name, key)
@@ -423,6 +502,7 @@ class ExpertCapture:
                 and ti.numel() % max(x.numel() // x.shape[-1], 1) == 0
             )
             self._routed[name] = bool(ok)
+            self._last_in[name] = {}
             if ok:
                 self.stashes[ik].add_routed(x, ti)
             if ik is not None and isinstance(x, torch.Tensor):
@@ -445,10 +525,24 @@ class ExpertCapture:
                     if hit is not None:
                         key, e, name = hit
                         st = self.cap.stashes[key]
-                        is_input = self.cap.params[key][1] in _INPUT_PARAMS
-                        if w.shape[-1] == st.in_features and not (is_input and self.cap._routed.get(name)):
+                        if w.shape[-1] == st.in_features and self.cap._take(key, e, name, args[0]):
                             st.add_rows(e, args[0])
             return func(*args, **kwargs)
+
+    def _take(self, key: str, e: int, name: str, x) -> bool:
+        """Whether an expert slice's F.linear input is stored: always for
+        ``down_proj``; for the input parameters only when the module call
+        was not routed through the pre-hook, and only once per tensor and
+        expert in one call."""
+        if self.params[key][1] not in _INPUT_PARAMS:
+            return True
+        if self._routed.get(name):
+            return False
+        seen = self._last_in.setdefault(name, {})
+        if seen.get(e) is x:
+            return False
+        seen[e] = x
+        return True
 
     def __enter__(self):
         for name, mod in self._modules.items():
@@ -465,6 +559,7 @@ class ExpertCapture:
         for h in self._hooks:
             h.remove()
         self._hooks.clear()
+        self._last_in.clear()
         return False
 
     # ---- results ----------------------------------------------------------
@@ -540,3 +635,223 @@ class ExpertCapture:
             st.clear()
         for st in self._samples.values():
             st.clear()
+
+
+# --------------------------------------------------------------------------
+# The reference's capture interface for one decoder layer (capture.py:82-343)
+# --------------------------------------------------------------------------
+
+
+@dataclass
+class LinearTask:
+    """An ``nn.Linear`` of the layer to quantize (capture.py:82-87).
+    ``stash_key`` names the stash holding its input rows; the same-input
+    dedup re-points it at a sibling's stash."""
+
+    name: str
+    module: torch.nn.Module
+    stash_key: str
+
+
+@dataclass
+class FusedExpertTask:
+    """One fused 3D expert parameter [E, out, in], quantized per expert
+    (capture.py:90-97). ``stash_keys[e]`` is ``"{module_name}.{param_name}::e{e}"``."""
+
+    module_name: str
+    param_name: str
+    param: torch.nn.Parameter
+    num_experts: int
+    stash_keys: list[str] = field(default_factory=list)
+
+
+class ExpertRows:
+    """Expert `expert`'s rows of a ``RoutedStash``, behind the per-expert
+    ``Stash`` interface the reference's callers use (``hessian``,
+    ``tokens``, ``chunks``, ``add``, ``nbytes``, ``clear``). No rows are
+    copied out: ``hessian`` is served from the stash's grouped launch."""
+
+    def __init__(self, routed: RoutedStash, expert: int, name: str):
+        self.routed = routed
+        self.expert = int(expert)
+        self.name = name
+        self.in_features = routed.in_features
+
+    @property
+    def tokens(self) -> int:
+        return int(self.routed.token_counts()[self.expert])
+
+    @property
+    def chunks(self) -> list[torch.Tensor]:
+        """This expert's rows, gathered into one bf16 [tokens, C] matrix."""
+        if self.tokens == 0:
+            return []
+        return [self.routed.expert_rows(self.expert)]
+
+    def add(self, x: torch.Tensor):
+        self.routed.add_rows(self.expert, x)
+
+    def add_sampled(self, x: torch.Tensor, max_rows: int):
+        rows = x.detach().reshape(-1, x.shape[-1])
+        if rows.shape[0] > max_rows:
+            idx = torch.linspace(0, rows.shape[0] - 1, steps=max_rows, device=rows.device).long()
+            rows = rows.index_select(0, idx)
+        self.add(rows)
+
+    def nbytes(self) -> int:
+        return self.tokens * self.in_features * 2
+
+    @torch.no_grad()
+    def hessian(self, device, chunk_rows: int = 65536) -> torch.Tensor:
+        """H = X_e^T X_e in fp32 on `device` (capture.py:68-76)."""
+        return self.routed.expert_hessian(self.expert, _hip_device(device))
+
+    def clear(self):
+        self.routed.drop_expert(self.expert)
+
+
+class CaptureManager:
+    """All capture state and hooks of one decoder layer (capture.py:100-343).
+
+    Same constructor, attributes and methods as the reference, so the
+    Stage-A drivers (sequential.py:707-741, dflash2_calibrate.py:177-214)
+    run on it unchanged; rows stay in HBM instead of CPU bf16 stashes:
+
+    * ``nn.Linear`` modules (not matching ``exclude_regex``, in_features
+      divisible by ``group_size``) become ``LinearTask``s with a
+      ``Stash`` each; a forward pre-hook stores the module's input, once per
+      batch per input tensor -- q/k/v or gate/up called on the same tensor
+      share the first sibling's stash (the task's ``stash_key`` is
+      re-pointed, as the reference does).
+    * fused 3D expert parameters become ``FusedExpertTask``s captured by an
+      ``ExpertCapture`` (the block input stored once per batch with its
+      top-k ids); ``stashes["{module}.{param}::e{e}"]`` are ``ExpertRows``
+      views of it.
+
+    Fast paths beyond the reference: ``expert_hessians(task, device,
+    experts)`` for a span of experts in one launch, and
+    ``span_solve.solve_fused_task`` for the whole task.
+    """
+
+    def __init__(self, layer: torch.nn.Module, exclude_regex, group_size: int):
+        import re
+
+        self.layer = layer
+        self.group_size = int(group_size)
+        self.stashes: dict[str, Stash | ExpertRows] = {}
+        self.linear_tasks: list[LinearTask] = []
+        self.fused_tasks: list[FusedExpertTask] = []
+        self._hooks = []
+        self._batch_seen: dict[int, tuple[torch.Tensor, str]] = {}
+        excl = re.compile(exclude_regex) if exclude_regex else None
+        for name, mod in layer.named_modules():
+            if not isinstance(mod, torch.nn.Linear):
+                continue
+            if excl is not None and excl.search(name):
+                log.debug("excluding %s (matches exclude regex)", name)
+                continue
+            if mod.in_features % self.group_size != 0:
+                log.warning("skipping %s: in_features %d not divisible by group %d "
+                            "(stays unquantized)", name, mod.in_features, self.group_size)
+                continue
+            self.linear_tasks.append(LinearTask(name, mod, stash_key=name))
+            self.stashes.setdefault(name, Stash(name, mod.in_features))
+        self.experts = ExpertCapture(layer, self.group_size)
+        self._task_stash: dict[int, RoutedStash] = {}
+        for key, (mname, pname, p) in self.experts.params.items():
+            E = int(p.shape[0])
+            task = FusedExpertTask(mname, pname, p, E)
+            st = self.experts.stashes[key]
+            for e in range(E):
+                k = f"{mname}.{pname}::e{e}"
+                task.stash_keys.append(k)
+                self.stashes[k] = ExpertRows(st, e, k)
+            self._task_stash[id(task)] = st
+            self.fused_tasks.append(task)
+
+    @property
+    def fallback_experts(self) -> dict[str, str]:
+        """stash key -> "all_expert_inputs" for backfilled experts."""
+        out = {}
+        for k, v in self.experts.fallback_experts.items():
+            base, _, e = k.rpartition("::e")
+            mname, pname, _ = self.experts.params[base]
+            out[f"{mname}.{pname}::e{e}"] = v
+        return out
+
+    # ---- nn.Linear capture --------------------------------------------------
+
+    def _linear_hook(self, task: LinearTask):
+        def hook(mod, args, kwargs):
+            x = args[0] if args else kwargs.get("input")
+            seen = self._batch_seen.get(id(x))
+            if seen is not None and seen[0] is x:
+                task.stash_key = seen[1]  # a sibling already stored this tensor
+                return
+            self._batch_seen[id(x)] = (x, task.stash_key)
+            self.stashes[task.stash_key].add(x)
+        return hook
+
+    # ---- lifecycle -------------------------------------------------------------
+
+    def __enter__(self):
+        for t in self.linear_tasks:
+            self._hooks.append(t.module.register_forward_pre_hook(self._linear_hook(t),
+                                                                  with_kwargs=True))
+        self.experts.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        self.experts.__exit__(*exc)
+        for h in self._hooks:
+            h.remove()
+        self._hooks.clear()
+        self._batch_seen.clear()
+        return False
+
+    def begin_batch(self):
+        """A new calibration batch: input tensors seen so far no longer dedup."""
+        self._batch_seen.clear()
+
+    # ---- diagnostics and results ---------------------------------------------
+
+    def total_stash_bytes(self) -> int:
+        lin = sum(s.nbytes() for s in self.stashes.values() if isinstance(s, Stash))
+        routed = {id(st): st for st in self.experts.stashes.values()}
+        return lin + sum(st.nbytes() for st in routed.values())
+
+    def expert_token_stats(self) -> dict[str, tuple[int, int, int, int]]:
+        """"{module}.{param}" -> (min, median, max, zero_count) of tokens per
+        expert (capture.py:242-252)."""
+        out = {}
+        for t in self.fused_tasks:
+            c = np.sort(self._task_stash[id(t)].token_counts())
+            out[f"{t.module_name}.{t.param_name}"] = (int(c[0]), int(c[len(c) // 2]), int(c[-1]),
+                                                      int((c == 0).sum()))
+        return out
+
+    def backfill_unrouted_experts(self) -> dict[str, list[int]]:
+        """Activation-aware rows for never-routed experts (capture.py:254-322);
+        returns module name -> backfilled experts."""
+        return self.experts.backfill_unrouted_experts()
+
+    def check_capture_happened(self):
+        """Abort if a fused parameter received no rows at all (capture.py:328-337)."""
+        for t in self.fused_tasks:
+            if self._task_stash[id(t)].rows == 0:
+                raise RuntimeError(
+                    f"No tokens captured for fused experts {t.module_name}.{t.param_name}. "
+                    "The model is probably not using the eager experts implementation; "
+                    "load it with experts_implementation='eager'."
+                )
+
+    def expert_hessians(self, task: FusedExpertTask, device, experts: range | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+        """Stacked H of a span of the task's experts (fp32 [n, C, C]), one launch."""
+        return self._task_stash[id(task)].hessians(device, experts, out=out)
+
+    def drop_all(self):
+        for s in self.stashes.values():
+            if isinstance(s, Stash):
+                s.clear()
+        self.experts.drop_all()

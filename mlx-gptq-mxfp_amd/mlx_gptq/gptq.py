@@ -141,6 +141,25 @@ def _attempts_report(att_h: np.ndarray, B: int, damp: float, H: torch.Tensor, de
                            lambda idx, sl=sl: H[torch.as_tensor(idx, device=dev)][:, sl, sl])
 
 
+def _staged(W: torch.Tensor, H: torch.Tensor, w_dtype: torch.dtype | None = None):
+    """(W_d, H_d): W and H on the HIP device that solves them -- the one
+    either already lives on, else the current device -- contiguous, H in
+    float32 (W in ``w_dtype`` if given). Tensors that already qualify are
+    returned as they are, so in-place updates land in the caller's tensors;
+    the caller copies results back into the others. Raises if no HIP device
+    is visible: nothing here computes on the host."""
+    dev = nat.device_for(W, H)
+    if W.is_cuda and H.is_cuda and W.device != H.device:
+        raise RuntimeError(f"W on {W.device} but H on {H.device}")
+
+    def put(t, dt):
+        if t.device == dev and t.dtype == dt and t.is_contiguous():
+            return t
+        return t.to(device=dev, dtype=dt).contiguous()
+
+    return put(W, w_dtype or W.dtype), put(H, torch.float32)
+
+
 @torch.no_grad()
 def _gptq_quantize_mxfp_groupwise(W: torch.Tensor, H: torch.Tensor, mode: str, damp: float,
                                   algorithm: str):
@@ -151,9 +170,20 @@ def _gptq_quantize_mxfp_groupwise(W: torch.Tensor, H: torch.Tensor, mode: str, d
     """
     if algorithm not in ("groupwise", "safe-scale-search"):
         raise ValueError(f"unsupported MXFP GPTQ algorithm: {algorithm}")
-    _require_device(W, H)
-    q, scales, _ = _mxfp_solve(W, H, mode, damp, algorithm, W, False)
-    return q, scales, None, W, None
+    W_d, H_d = _staged(W, H)
+    _require_device(W_d, H_d)
+    q, scales, _ = _mxfp_solve(W_d, H_d, mode, damp, algorithm, W_d, False)
+    _write_back(W, W_d, H, H_d)
+    return q.to(W.device), scales.to(W.device), None, W, None
+
+
+def _write_back(W, W_d, H, H_d) -> None:
+    """Copy the in-place results (W_dq, the dead-column diagonals of H) from
+    the solving device's copies into the caller's tensors."""
+    if W_d is not W:
+        W.copy_(W_d)
+    if H_d is not H:
+        H.copy_(H_d)
 
 
 def _require_device(W: torch.Tensor, H: torch.Tensor) -> None:
@@ -189,6 +219,10 @@ def gptq_quantize(
     W: [B, out, in] float32 (overwritten with the dequantized weights),
     H: [B, in, in] float32 (dead-column diagonals set to 1 in place).
     Returns (q uint8, scales, biases | None, W_dq (= W), None).
+
+    W and H may live on the host (dflash2_calibrate.py:55-80 solves large
+    matrices from CPU tensors): they are solved on the current HIP device and
+    the results come back to W's device, W and H updated in place.
     """
     assert W.dim() == 3 and H.dim() == 3
     B, R, C = W.shape
@@ -196,17 +230,20 @@ def gptq_quantize(
     assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
     if mode in ("mxfp4", "mxfp8") and group_size != MX_GROUP_SIZE:
         raise ValueError(f"{mode} requires group size {MX_GROUP_SIZE}")
+    if W.dtype != torch.float32:
+        raise TypeError("gptq_quantize updates W in place and needs float32 W")
     if mode in ("mxfp4", "mxfp8"):
         if mxfp_algorithm == "auto":
             mxfp_algorithm = "safe-scale-search" if mode == "mxfp4" else "groupwise"
-        if W.dtype != torch.float32:
-            raise TypeError("gptq_quantize updates W in place and needs float32 W")
         return _gptq_quantize_mxfp_groupwise(W, H, mode, damp, mxfp_algorithm)
     # any other mode string takes the affine path, as in the reference
     from . import gptq_affine
 
-    return gptq_affine.gptq_quantize_affine(W, H, bits, group_size, damp, clip, storage_dtype,
-                                            block_size)
+    W_d, H_d = _staged(W, H)
+    q, s, b, _, _ = gptq_affine.gptq_quantize_affine(W_d, H_d, bits, group_size, damp, clip,
+                                                     storage_dtype, block_size)
+    _write_back(W, W_d, H, H_d)
+    return q.to(W.device), s.to(W.device), b.to(W.device), W, None
 
 
 @torch.no_grad()
@@ -221,7 +258,12 @@ def solve_gptq(
     mode: str = "affine",
     mxfp_algorithm: str = "auto",
 ):
-    """Keep W_orig intact, return (q, scales, biases, W_dq, rel_err[B]) (gptq.py:275-302)."""
+    """Keep W_orig intact, return (q, scales, biases, W_dq, rel_err[B]) (gptq.py:275-302).
+
+    Host tensors are solved on the current HIP device; every output is
+    returned on W_orig's device and H gets the dead-column fix in place,
+    as the reference's device-agnostic torch code does."""
+    out_dev = W_orig.device
     if mode in ("mxfp4", "mxfp8"):
         assert W_orig.dim() == 3 and H.dim() == 3
         B, R, C = W_orig.shape
@@ -231,16 +273,24 @@ def solve_gptq(
             raise ValueError(f"{mode} requires group size {MX_GROUP_SIZE}")
         if mxfp_algorithm == "auto":
             mxfp_algorithm = "safe-scale-search" if mode == "mxfp4" else "groupwise"
-        src = W_orig if W_orig.dtype in (torch.float32, torch.bfloat16, torch.float16) else W_orig.float()
-        src = src.contiguous()
-        _require_device(src, H)
+        # bf16 / f16 weights are read as they are (their float() is exact)
+        wdt = W_orig.dtype if W_orig.dtype in (torch.float32, torch.bfloat16, torch.float16) \
+            else torch.float32
+        src, H_d = _staged(W_orig, H, wdt)
+        _require_device(src, H_d)
         W_dq = torch.empty(B, R, C, dtype=torch.float32, device=src.device)
-        q, s, rel = _mxfp_solve(src, H, mode, damp, mxfp_algorithm, W_dq, True)
-        return q, s, None, W_dq, rel
-    W = W_orig.float().clone()
-    q, s, b, W_dq, _ = gptq_quantize(W, H, bits, group_size, damp=damp, clip=clip,
-                                     storage_dtype=storage_dtype, mode=mode,
-                                     mxfp_algorithm=mxfp_algorithm)
+        q, s, rel = _mxfp_solve(src, H_d, mode, damp, mxfp_algorithm, W_dq, True)
+        if H_d is not H:
+            H.copy_(H_d)
+        return q.to(out_dev), s.to(out_dev), None, W_dq.to(out_dev), rel.to(out_dev)
     from . import gptq_affine
 
-    return q, s, b, W_dq, gptq_affine.rel_err(W_dq, W_orig)
+    W0, H_d = _staged(W_orig, H)
+    W = W0.float().clone()
+    q, s, b, W_dq, _ = gptq_quantize(W, H_d, bits, group_size, damp=damp, clip=clip,
+                                     storage_dtype=storage_dtype, mode=mode,
+                                     mxfp_algorithm=mxfp_algorithm)
+    rel = gptq_affine.rel_err(W_dq, W0)
+    if H_d is not H:
+        H.copy_(H_d)
+    return q.to(out_dev), s.to(out_dev), b.to(out_dev), W_dq.to(out_dev), rel.to(out_dev)

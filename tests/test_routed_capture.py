@@ -278,3 +278,74 @@ def test_gpu_routed_stash_empty_experts_and_cpu_rows():
             assert bool((H[e] == 0).all())
         else:
             assert _rel(H[e].cpu(), ref) < 1e-5
+
+
+class _SeparateGateUp(torch.nn.Module):
+    """Fused experts with separate 3D gate_proj / up_proj parameters, routed
+    internally (no top_k_index): both slices' F.linear calls see the same
+    input tensor, which must be stored once per expert."""
+
+    def __init__(self, E=4, hidden=32, inter=16):
+        super().__init__()
+        g = torch.Generator().manual_seed(6)
+        self.gate_proj = torch.nn.Parameter(torch.randn(E, inter, hidden, generator=g) * 0.2)
+        self.up_proj = torch.nn.Parameter(torch.randn(E, inter, hidden, generator=g) * 0.2)
+        self.down_proj = torch.nn.Parameter(torch.randn(E, hidden, inter, generator=g) * 0.2)
+
+    def forward(self, hidden_states):
+        out = torch.zeros_like(hidden_states)
+        route = hidden_states[:, 0].abs().mul(100).long() % self.gate_proj.shape[0]
+        for e in range(self.gate_proj.shape[0]):
+            idx = torch.nonzero(route == e).flatten()
+            if idx.numel() == 0:
+                continue
+            x = hidden_states[idx]
+            h = F.silu(F.linear(x, self.gate_proj[e])) * F.linear(x, self.up_proj[e])
+            out[idx] = F.linear(h, self.down_proj[e])
+        return out
+
+
+def test_separate_gate_up_fallback_stores_each_row_once():
+    m = _SeparateGateUp()
+    cap = capture.ExpertCapture(m)
+    rec = _Recorder(type("B", (), {"experts": m})())
+    g = torch.Generator().manual_seed(4)
+    with torch.no_grad(), cap, rec:
+        for _ in range(3):
+            m(torch.randn(11, 32, generator=g))
+    st = cap.stashes["gate_proj"]
+    assert st is cap.stashes["up_proj"]
+    assert st.rows == 33  # not 66: the up_proj call repeats the gate_proj input
+    for e in range(4):
+        assert torch.equal(st.expert_rows(e), _recorded(rec, "gate_proj", e, 32))
+        assert torch.equal(st.expert_rows(e), _recorded(rec, "up_proj", e, 32))
+        assert torch.equal(cap.stashes["down_proj"].expert_rows(e), _recorded(rec, "down_proj", e, 16))
+
+
+def test_empty_batch_routes_nothing():
+    st = capture.RoutedStash("s", 8, 3)
+    st.add_routed(torch.zeros(0, 8), torch.zeros(0, 2, dtype=torch.int64))
+    st.add_routed(torch.zeros(1, 0, 8), torch.zeros(0, 2, dtype=torch.int64))
+    assert st.rows == 0 and st.token_counts().tolist() == [0, 0, 0]
+    st.add_rows(1, torch.zeros(0, 8))
+    st.add_routed(torch.ones(2, 8), torch.tensor([[0, 2], [2, 2]]))
+    assert st.token_counts().tolist() == [1, 0, 3]
+    blk = _block(E=4, k=2, hidden=32, inter=32)
+    cap = capture.ExpertCapture(blk)
+    with torch.no_grad(), cap:
+        blk(torch.zeros(1, 0, 32))  # an empty batch through the real block
+        blk(torch.randn(1, 5, 32))
+    assert cap.stashes["experts.gate_up_proj"].rows == 5
+
+
+def test_drop_expert_forgets_only_that_expert():
+    st = capture.RoutedStash("s", 4, 3)
+    x = torch.arange(12, dtype=torch.float32).reshape(3, 4)
+    st.add_routed(x, torch.tensor([[0, 1], [1, 2], [2, 0]]))
+    assert st.token_counts().tolist() == [2, 2, 2]
+    st.drop_expert(1)
+    assert st.token_counts().tolist() == [2, 0, 2]
+    st.add_rows(1, torch.ones(1, 4))  # rows added after the drop count
+    assert st.token_counts().tolist() == [2, 1, 2]
+    assert torch.equal(st.expert_rows(1), torch.ones(1, 4, dtype=torch.bfloat16))
+    assert sorted(st.expert_rows(0)[:, 0].tolist()) == [0.0, 8.0]

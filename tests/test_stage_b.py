@@ -141,7 +141,8 @@ def test_gpu_inject_errors(tmp_path):
     _model(tmp_path / "m2", {key: torch.zeros(2, 4, dtype=torch.uint32),
                              "model.layers.0.proj.scales": torch.zeros(2, 1, dtype=torch.uint8)},
            {"mode": "mxfp8", "bits": 8, "group_size": 32})
-    with pytest.raises(RuntimeError, match="model config expects mxfp8/8b/g32"):
+    # a dense tensor's mismatch uses the reference's short form (pack.py:163-173)
+    with pytest.raises(RuntimeError, match="artifact mxfp4/4b/g32 vs config mxfp8/8b/g32"):
         pack.inject(str(tmp_path / "m2"), reader)
     _model(tmp_path / "m3", {key: torch.zeros(2, 4, dtype=torch.uint32),
                              "model.layers.0.proj.scales": torch.zeros(2, 1, dtype=torch.uint8)},
