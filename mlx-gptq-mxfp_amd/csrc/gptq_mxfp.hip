@@ -20,9 +20,11 @@
 //      RTN candidate's;
 //   4. range guard: every |dq| <= max(32 * max|orig|, 2^-126), else the RTN
 //      baseline at the chosen scale.
-// Objectives are fp32 sums in a fixed order (not torch's einsum order), so
-// near-exact ties between candidates may resolve differently from the
-// reference; every encoding itself is bit-exact.
+// Objectives have fp32 accuracy (exact bf16 x bf16 products of three-way
+// split operands, fp32 accumulation) but a fixed summation order, not
+// torch's einsum order, so ties within a few fp32 ulps between candidates
+// may resolve differently from the reference; every encoding itself is
+// bit-exact.
 #include <type_traits>
 
 #include "mgq_capi.h"
@@ -94,15 +96,21 @@ __device__ inline void quant_err8(const float (&w)[8], float scale, float inv_sc
 
 // e^T Hg e on the matrix cores, for the 64 rows of a wave at once.
 //
-// P^T = Hg E^T is a 32x32 by 32x64 product: two 32-row blocks of E, each two
-// v_mfma_f32_32x32x16_bf16 over K = 32. Operands are split into bf16 hi + lo
-// (x = hi + lo within ~2^-17 relative) and the product is accumulated as
-// hi*hi + hi*lo + lo*hi in fp32, so the objective carries ~2^-16 relative
-// error against an fp32 sum (candidate choices only differ on near-ties).
+// P^T = Hg E^T is a 32x32 by 32x64 product: two 32-row blocks of E, each
+// v_mfma_f32_32x32x16_bf16 over K = 32. Every fp32 operand is split into
+// three bf16 parts, x = x1 + x2 + x3 exactly (each part holds the next 8
+// significant bits; exact for |x| >= 2^-100), and the product is
+// accumulated in fp32 from the partial products that carry more than 2^-24
+// of the result: h1 e1, h1 e2, h2 e1, h1 e3, h2 e2, h3 e1 (each bf16 x bf16
+// product is exact). The objective therefore has the accuracy of an fp32
+// sum, as the reference's fp32 einsum (gptq.py:123-125,168); only its
+// summation order differs.
 // Layouts (32x32x16 bf16): A lane l = row l%32, k = 8(l/32)+0..7; B lane l =
 // k = 8(l/32)+0..7, column l%32; D lane l register r = row 8(r/4)+4(l/32)+
 // r%4, column l%32.
-//   - A = Hg: lane l holds Hg[l%32][16kc + 8(l/32) + 0..7] (built once).
+//   - A = Hg: lane l needs Hg[l%32][16kc + 8(l/32) + 0..7]; the three parts
+//     of the workgroup's block are staged in LDS (HSplit) in exactly that
+//     order, so each operand is one conflict-free 16-byte read per lane.
 //   - B = E^T of a 32-row block: lane l needs row l%32 of the block, columns
 //     16kc + 8(l/32) + 0..7. Each lane owns its own row's e[]; one
 //     v_permlane32_swap of (e[16kc..+7], e[16kc+8..+15]) yields block 0's B
@@ -116,30 +124,49 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-struct HOperand {
-  bf16x8_t hi[2], lo[2];
+// The three bf16 parts of a 32x32 Hessian block in the A-operand order:
+// part p, K-chunk kc, row c, half h = the 8 values Hg[c][16kc + 8h + 0..7].
+struct HSplit {
+  u32x4_t v[3][2][kG][2];
 };
 
-__device__ inline void split_bf16(const float* x, bf16x8_t& hi, bf16x8_t& lo) {
+__device__ inline void split3(float x, __bf16& a, __bf16& b, __bf16& c) {
+  a = static_cast<__bf16>(x);
+  const float r = x - static_cast<float>(a);  // exact
+  b = static_cast<__bf16>(r);
+  c = static_cast<__bf16>(r - static_cast<float>(b));  // exact, and exact in bf16
+}
+
+__device__ inline void split3x8(const float* x, bf16x8_t& a, bf16x8_t& b, bf16x8_t& c) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const __bf16 h = static_cast<__bf16>(x[j]);
-    hi[j] = h;
-    lo[j] = static_cast<__bf16>(x[j] - static_cast<float>(h));
+    __bf16 p, q, r;
+    split3(x[j], p, q, r);
+    a[j] = p;
+    b[j] = q;
+    c[j] = r;
   }
 }
 
-__device__ inline HOperand load_h_operand(const float* __restrict__ Hg, int lane) {
-  HOperand A;
-  const int c = lane & 31, k8 = 8 * (lane >> 5);
-#pragma unroll
-  for (int kc = 0; kc < 2; ++kc) {
+// Fill the workgroup's HSplit from the compact Hessian block (row-major
+// 32x32 fp32); threads 0..127 each build one (kc, row, half) chunk.
+__device__ inline void stage_hsplit(const float* __restrict__ Hg, HSplit* hs) {
+  const int t = threadIdx.x;
+  if (t < 2 * kG * 2) {
+    const int kc = t / (2 * kG), c = (t / 2) % kG, h = t & 1;
     float x[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = Hg[c * kG + 16 * kc + k8 + j];
-    split_bf16(x, A.hi[kc], A.lo[kc]);
+    for (int j = 0; j < 8; ++j) x[j] = Hg[c * kG + 16 * kc + 8 * h + j];
+    bf16x8_t a, b, d;
+    split3x8(x, a, b, d);
+    hs->v[0][kc][c][h] = __builtin_bit_cast(u32x4_t, a);
+    hs->v[1][kc][c][h] = __builtin_bit_cast(u32x4_t, b);
+    hs->v[2][kc][c][h] = __builtin_bit_cast(u32x4_t, d);
   }
-  return A;
+}
+
+__device__ inline bf16x8_t h_part(const HSplit* hs, int p, int kc, int lane) {
+  return __builtin_bit_cast(bf16x8_t, hs->v[p][kc][lane & 31][lane >> 5]);
 }
 
 // (x, y) -> ([x lanes 0-31 | y lanes 0-31], [x lanes 32-63 | y lanes 32-63])
@@ -155,24 +182,9 @@ __device__ inline void swap_halves(bf16x8_t& x, bf16x8_t& y) {
   y = __builtin_bit_cast(bf16x8_t, b);
 }
 
-__device__ inline float mfma_objective(const float (&e)[kG], const HOperand& A) {
-  f32x16_t d0, d1;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) d0[r] = d1[r] = 0.0f;
-#pragma unroll
-  for (int kc = 0; kc < 2; ++kc) {
-    bf16x8_t xh, xl, yh, yl;
-    split_bf16(e + 16 * kc, xh, xl);
-    split_bf16(e + 16 * kc + 8, yh, yl);
-    swap_halves(xh, yh);
-    swap_halves(xl, yl);
-    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], xh, d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], yh, d1, 0, 0, 0);
-    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], xl, d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], yl, d1, 0, 0, 0);
-    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], xh, d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], yh, d1, 0, 0, 0);
-  }
+// obj = sum_c e[c] P[c] from the two accumulator blocks
+__device__ inline float objective_from(const float (&e)[kG], const f32x16_t& d0,
+                                       const f32x16_t& d1) {
   float obj = 0.0f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -185,13 +197,40 @@ __device__ inline float mfma_objective(const float (&e)[kG], const HOperand& A) 
   return obj;
 }
 
+#define MGQ_MFMA2(A, X, Y)                                          \
+  d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16((A), (X), d0, 0, 0, 0); \
+  d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16((A), (Y), d1, 0, 0, 0)
+
+__device__ inline float mfma_objective(const float (&e)[kG], const HSplit* hs, int lane) {
+  f32x16_t d0, d1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d0[r] = d1[r] = 0.0f;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    bf16x8_t x1, x2, x3, y1, y2, y3;
+    split3x8(e + 16 * kc, x1, x2, x3);
+    split3x8(e + 16 * kc + 8, y1, y2, y3);
+    swap_halves(x1, y1);
+    swap_halves(x2, y2);
+    swap_halves(x3, y3);
+    const bf16x8_t h1 = h_part(hs, 0, kc, lane), h2 = h_part(hs, 1, kc, lane),
+                   h3 = h_part(hs, 2, kc, lane);
+    // the nonzero products in the order mfma_objective_x1 adds them when
+    // e2 = e3 = 0 (h1 e1, h2 e1, h3 e1), so both give the same bits then
+    MGQ_MFMA2(h1, x1, y1);
+    MGQ_MFMA2(h1, x2, y2);
+    MGQ_MFMA2(h2, x1, y1);
+    MGQ_MFMA2(h1, x3, y3);
+    MGQ_MFMA2(h2, x2, y2);
+    MGQ_MFMA2(h3, x1, y1);
+  }
+  return objective_from(e, d0, d1);
+}
+
 // The same objective when every e[c] is exactly a bf16 value (bf16 weights
 // and candidate scales whose |w / scale| stays below 512 for MXFP4, 16384
-// for MXFP8): E is one exact bf16 operand, so the hi*lo products of
-// mfma_objective are zero and are skipped. The non-zero products are
-// accumulated in the same order, so both functions return the same bits for
-// the same errors.
-__device__ inline float mfma_objective_x1(const float (&e)[kG], const HOperand& A) {
+// for MXFP8): E is one exact bf16 operand and only h1 e, h2 e, h3 e remain.
+__device__ inline float mfma_objective_x1(const float (&e)[kG], const HSplit* hs, int lane) {
   f32x16_t d0, d1;
 #pragma unroll
   for (int r = 0; r < 16; ++r) d0[r] = d1[r] = 0.0f;
@@ -204,22 +243,13 @@ __device__ inline float mfma_objective_x1(const float (&e)[kG], const HOperand& 
       y[j] = static_cast<__bf16>(e[16 * kc + 8 + j]);
     }
     swap_halves(x, y);
-    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], x, d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.hi[kc], y, d1, 0, 0, 0);
-    d0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], x, d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.lo[kc], y, d1, 0, 0, 0);
+    MGQ_MFMA2(h_part(hs, 0, kc, lane), x, y);
+    MGQ_MFMA2(h_part(hs, 1, kc, lane), x, y);
+    MGQ_MFMA2(h_part(hs, 2, kc, lane), x, y);
   }
-  float obj = 0.0f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(d0[r]), __float_as_uint(d1[r]),
-                                                     false, false);
-    const int c0 = 8 * (r >> 2) + (r & 3);
-    obj = fmaf(e[c0], __uint_as_float(sw[0]), obj);
-    obj = fmaf(e[c0 + 4], __uint_as_float(sw[1]), obj);
-  }
-  return obj;
+  return objective_from(e, d0, d1);
 }
+#undef MGQ_MFMA2
 
 // An opaque zero that depends on `v`: addresses built from it cannot be
 // computed before `v`, so the loads behind them are neither hoisted out of
@@ -242,6 +272,27 @@ __device__ inline const lds_f32* lds_after(const lds_f32* p, float dep) {
   uint32_t a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
   asm volatile("; lds_after %1" : "+v"(a) : "v"(dep));
   return reinterpret_cast<const lds_f32*>(static_cast<uintptr_t>(a));
+}
+
+// value(code) of the code in byte k of `word` (one code per byte), on the
+// hardware decode at scale 1 (k is a constant once the callers unroll).
+template <int MODE>
+__device__ inline float decode_code(uint32_t word, int k) {
+  if constexpr (MODE == kMxfp4) {
+    switch (k) {
+      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0)[0];
+      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1)[0];
+      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2)[0];
+      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3)[0];
+    }
+  } else {
+    switch (k) {
+      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, false)[0];
+      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, false)[1];
+      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, true)[0];
+      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, true)[1];
+    }
+  }
 }
 
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
@@ -303,10 +354,17 @@ __global__ void __launch_bounds__(kThreads)
   __shared__ float Ut[kG * kG];
   // RN(1/U[c][c]) for the correctly rounded divisions of the recurrence
   __shared__ float ydiag[kG];
+  // the safe search's objective operand: Hg as three exact bf16 parts
+  HSplit* hs = nullptr;
+  if constexpr (SAFE) {
+    __shared__ HSplit hsplit_s;
+    hs = &hsplit_s;
+  }
   {
     const float* Ub = U + (b * G + g) * kG * kG;
     for (int e = threadIdx.x; e < kG * kG; e += kThreads) Ut[(e % kG) * kG + e / kG] = Ub[e];
     if (threadIdx.x < kG) ydiag[threadIdx.x] = div_exact_recip(Ub[threadIdx.x * (kG + 1)]);
+    if constexpr (SAFE) stage_hsplit(Hg, hs);
   }
   __syncthreads();
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
@@ -360,36 +418,23 @@ __global__ void __launch_bounds__(kThreads)
     return o[(i / 2) * 2 * kThreads + (i & 1)];
   };
 #define ORIG(i) orig_at(orig, (i))
-  // The dequantized values of the selected result: in LDS for the safe
-  // search, whose candidate objectives need the registers; in registers for
-  // the groupwise solve. MXFP4 values (at most 2 significant bits times a
-  // power of two >= 2^-128) are exact in bf16 and are stored as the top half
-  // of their fp32 bits; MXFP8 stores the E4M3 code and decodes it on read
-  // (value(code) * scale, what the encoder returned).
-  using DqT = std::conditional_t<MODE == kMxfp4, uint16_t, uint8_t>;
+  // The selected result's codes, one per byte (codes[i / 4] byte i % 4),
+  // kept in registers until the final store. The safe search, whose
+  // candidate objectives need the registers, reads its dequantized values
+  // back from them: value(code) * scale on the hardware decode, the same
+  // product the encoder returned. The groupwise solve keeps them in
+  // registers as they come.
+  uint32_t codes[kG / 4];
   float dqr[SAFE ? 1 : kG];
-  DqT* dqs = nullptr;
-  if constexpr (SAFE) {
-    __shared__ DqT sdq[kG * kThreads];
-    dqs = sdq + threadIdx.x;
-  }
   float dq_scale = 0.0f;  // the selected scale, set before the first read
   auto dq_get = [&](int i) __attribute__((always_inline)) -> float {
     if constexpr (!SAFE)
       return dqr[i];
-    else if constexpr (MODE == kMxfp4)
-      return bf16_to_f32(dqs[i * kThreads]);
     else
-      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(static_cast<uint32_t>(dqs[i * kThreads]), 1.0f,
-                                                      false)[0] * dq_scale;
+      return decode_code<MODE>(codes[i / 4], i % 4) * dq_scale;
   };
-  auto dq_set = [&](int i, float v, uint32_t code) __attribute__((always_inline)) {
-    if constexpr (!SAFE)
-      dqr[i] = v;
-    else if constexpr (MODE == kMxfp4)
-      dqs[i * kThreads] = static_cast<uint16_t>(f2u(v) >> 16);
-    else
-      dqs[i * kThreads] = static_cast<uint8_t>(code);
+  auto dq_set = [&](int i, float v) __attribute__((always_inline)) {
+    if constexpr (!SAFE) dqr[i] = v;
   };
 #define DQ(i) dq_get(i)
 
@@ -401,7 +446,6 @@ __global__ void __launch_bounds__(kThreads)
   // of the scaled objectives, without scaling every error.
   float best = 0.0f;
   if (SAFE) {
-    const HOperand Ah = load_h_operand(Hg, lane);
     float err[kG];
     for (int o = 0; o < offs.n; ++o) {
       int e = e0 + offs.v[o];
@@ -421,7 +465,7 @@ __global__ void __launch_bounds__(kThreads)
         quant_err8<MODE>(x, sc, inv, lim, err + 2 * p0);
         __builtin_amdgcn_sched_barrier(0);
       }
-      const float raw = XERR ? mfma_objective_x1(err, Ah) : mfma_objective(err, Ah);
+      const float raw = XERR ? mfma_objective_x1(err, hs, lane) : mfma_objective(err, hs, lane);
       const float obj = raw * exp2_int(2 * (e - e0));
       if (o == 0 || obj < best) {
         best = obj;
@@ -438,9 +482,7 @@ __global__ void __launch_bounds__(kThreads)
   // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
   // Forming w_c lazily from the stored errors performs exactly those
   // roundings while keeping only err[] live.
-  // The dequantized values go to LDS (DQ), which keeps 32 registers free.
   float errs[kG];
-  uint32_t codes[kG / 4];
 #pragma unroll
   for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
@@ -459,7 +501,7 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
     errs[c] = div_exact(acc - dq, col[c], ydiag[c]);  // = (acc - dq) / U[c][c]
     codes[c / 4] |= code << (8 * (c % 4));
-    dq_set(c, dq, code);
+    dq_set(c, dq);
   }
 
   // 3. GPTQ vs best RTN candidate (safe search only)
@@ -472,10 +514,7 @@ __global__ void __launch_bounds__(kThreads)
       for (int i = i0; i < i0 + 8; ++i) err[i] = (DQ(i) - ORIG(i)) * inv_scale;
       __builtin_amdgcn_sched_barrier(0);
     }
-    // the H operand again (an opaque offset: a fresh load, not registers held
-    // through the recurrence)
-    const HOperand Ah2 = load_h_operand(Hg + zero_after(err[0]), lane);
-    use_gptq = mfma_objective(err, Ah2) * exp2_int(2 * (e_sel - e0)) <= best;
+    use_gptq = mfma_objective(err, hs, lane) * exp2_int(2 * (e_sel - e0)) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;
@@ -494,7 +533,7 @@ __global__ void __launch_bounds__(kThreads)
       float dq;
       const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
       codes[i / 4] |= code << (8 * (i % 4));
-      dq_set(i, dq, code);
+      dq_set(i, dq);
     }
   }
   float w[kG];

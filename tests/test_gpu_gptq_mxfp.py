@@ -56,7 +56,8 @@ def test_mxfp_matches_reference_golden(name):
     assert b is None and s.dtype == torch.uint8
     assert torch.equal(Hd.cpu(), t[f"{name}.H_after"])
     assert _agree(q, t[f"{name}.q"]) >= 0.995
-    assert _agree(s, t[f"{name}.scales"]) >= 0.99
+    # groupwise scales are choose_mxfp_scale of the weights: deterministic
+    assert _agree(s, t[f"{name}.scales"]) >= (1.0 if kw["mxfp_algorithm"] == "groupwise" else 0.99)
     # W_dq is exactly the decode of (q, scales)
     assert torch.equal(grid.dequantize_artifact(q, s, None, kw["mode"], 32), W_dq)
     Href = t[f"{name}.H_after"]
@@ -82,7 +83,7 @@ def test_mxfp_matches_oracle_larger(mode, alg):
                                               mxfp_algorithm=alg)
     assert torch.equal(Hg.cpu(), Hr)
     assert _agree(q, rq) >= 0.995
-    assert _agree(s, rs) >= 0.99
+    assert _agree(s, rs) >= (1.0 if alg == "groupwise" else 0.99)
     pl, pl_ref = _proxy(W.to(torch.bfloat16).float(), W_dq, Hr), _proxy(W.to(torch.bfloat16).float(), rW, Hr)
     assert torch.all((pl - pl_ref).abs() <= 0.01 * pl_ref.abs()), (pl, pl_ref)
 
