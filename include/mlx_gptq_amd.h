@@ -241,6 +241,24 @@ int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_
                         uint8_t* scales_out, float* W_dq, float* rel_err, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of mgq_gptq_mxfp. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results as mgq_gptq_mxfp without the
+ * workspace: the solver's scratch is a fixed per-GPU device array of
+ * mgq_noalloc_scratch_bytes() bytes (32 MiB) that the library holds on every
+ * GPU it runs on until the process ends. Calls needing more than that
+ * (mgq_gptq_mxfp_workspace_size(B, R, C)) fail with MGQ_ERR_WORKSPACE before
+ * anything is launched; split the batch. The stream must belong to the
+ * current device. All calls on one GPU share its array: calls that overlap
+ * on one GPU race and must be serialised by the caller. Allocates nothing. */
+int64_t mgq_noalloc_scratch_bytes(void);
+int mgq_gptq_mxfp_noalloc(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, float* H,
+                          int mode, int algorithm, float damp, int max_attempts,
+                          const int32_t* offsets, int n_offsets, uint8_t* q_out,
+                          uint8_t* scales_out, float* W_dq, float* rel_err, int32_t* attempts,
+                          void* stream);
+
 /* Workspace bytes needed by mgq_hinv_full_pass for H [B, C, C] (two fp64
  * [B, C, C] arrays). */
 int64_t mgq_hinv_full_workspace_size(int64_t B, int64_t C);

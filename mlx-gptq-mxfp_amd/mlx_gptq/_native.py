@@ -70,6 +70,9 @@ SIGNATURES: dict[str, list] = {
     "mgq_gptq_mxfp_workspace_size": [_I64, _I64, _I64],
     "mgq_gptq_mxfp": [_VP, _INT, _I64, _I64, _I64, _VP, _INT, _INT, _F32, _INT, _VP, _INT,
                       _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP],
+    "mgq_noalloc_scratch_bytes": [],
+    "mgq_gptq_mxfp_noalloc": [_VP, _INT, _I64, _I64, _I64, _VP, _INT, _INT, _F32, _INT, _VP, _INT,
+                              _VP, _VP, _VP, _VP, _VP, _VP],
     "mgq_gptq_mxfp_prepare": [_VP, _I64, _I64, _I64, _F32, _INT, _VP, _VP, _I64, _VP],
     "mgq_gptq_mxfp_solve": [_VP, _INT, _I64, _I64, _I64, _INT, _INT, _VP, _INT, _VP, _VP, _VP,
                             _VP, _VP, _I64, _VP],
@@ -83,6 +86,7 @@ SIGNATURES: dict[str, list] = {
 _RESTYPES = {
     "mgq_last_error": ctypes.c_char_p,
     "mgq_gptq_mxfp_workspace_size": ctypes.c_int64,
+    "mgq_noalloc_scratch_bytes": ctypes.c_int64,
     "mgq_hinv_full_workspace_size": ctypes.c_int64,
 }
 
