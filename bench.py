@@ -79,6 +79,19 @@ def _traffic(name: str, kernel_prefix: str):
     return round(float(max(hits))) if hits else None
 
 
+def _counter(name: str, kernel_prefix: str, key: str):
+    """A per-dispatch rocprofv3 counter figure of a kernel (e.g. its MFMA
+    util %) as committed under profiles/<name>_counters.json; None if
+    absent."""
+    p = os.path.join(ROOT, "profiles", f"{name}_counters.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        per = json.load(f).get("per_dispatch", {})
+    hits = [v[key] for k, v in per.items() if k.startswith(kernel_prefix) and key in v]
+    return max(hits) if hits else None
+
+
 def _roofline(kernel, bound, amount, ms, traffic=None):
     """amount: flops (bound "mfma": bf16 MFMA peak; "fp64": fp64 peak) or bytes
     (bound "hbm") per launch."""
@@ -109,13 +122,17 @@ def _timed(torch, np, step, n_phase, warmup, steps):
         step()
     torch.cuda.synchronize()
     phase = np.zeros(n_phase)
+    per_step = []
     t0 = time.perf_counter()
     out = None
     for _ in range(steps):
+        ts = time.perf_counter()
         out, evs = step()
         torch.cuda.synchronize()  # events of this step are complete
+        per_step.append((time.perf_counter() - ts) * 1e3)
         phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(n_phase)]
     t1 = time.perf_counter()
+    _timed.median_ms = float(np.median(per_step)) if per_step else 0.0
     return out, (t1 - t0) * 1e3 / steps, phase / steps
 
 
@@ -128,6 +145,7 @@ def _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, extra=No
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 3),
+        "ms_per_step_median": round(getattr(_timed, "median_ms", ms_step), 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -188,7 +206,7 @@ def run_moe(args, torch, np) -> int:
     roofline = _roofline("syrk_kernel (gate_up Hessian, routed gather)", "mfma",
                          A * hidden * (hidden + 1),  # SYRK count N*C*(C+1)
                          float(phase[0]), _traffic("bench_moe_cfg4", "mgq::syrk_kernel<true"))
-    cpu = _cpu_baseline_moe(L, ne, out, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = _cpu_baseline_moe(L, ne, out, args.cpu_seconds, (H_gu, H_dn)) if args.cpu_seconds > 0 else None
     config = {
         "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
                     "[2048,768]), 131072 tokens top-8, MXFP4 safe-scale-search GPTQ, 4 unrouted "
@@ -198,7 +216,13 @@ def run_moe(args, torch, np) -> int:
     }
     phases = {"hessian_gate_up": phase[0], "hessian_down": phase[1], "solve_gate_up": phase[2],
               "solve_down": phase[3], "rtn_and_pack": phase[4]}
-    _line(args, value, ms_step, config, phases, roofline, cpu, setup_s)
+    # rocprofv3 MFMA-busy / active cycles of the two SYRK launches (the
+    # profiler cannot run inside this process: committed per-dispatch figures)
+    counters = {"hessian_mfma_util_pct": {
+        "gate_up": _counter("bench_moe_cfg4", "mgq::syrk_kernel<true", "mfma_util_pct"),
+        "down": _counter("bench_moe_cfg4", "mgq::syrk_kernel<false", "mfma_util_pct")},
+        "solve_valu_busy_pct": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel", "valu_busy_pct")}
+    _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, counters)
     return 0
 
 
@@ -329,6 +353,7 @@ def run_audit(args, torch, np) -> int:
         sys.path.insert(0, ROOT)
         from oracle import validate_ref
 
+        info = _cpu_setup(torch)
         rows = max(1, min(src.shape[0], 8192))
         s_c, q_c, b_c = src[:rows].cpu(), q[:rows].cpu(), sb[:rows].cpu()
         t0 = time.perf_counter()
@@ -336,7 +361,7 @@ def run_audit(args, torch, np) -> int:
         t1 = time.perf_counter()
         got = validate_artifacts.range_audit(src[:rows], q[:rows], sb[:rows], None, "mxfp4", 32)
         cpu = {"value": round(rows * src.shape[1] / (t1 - t0), 1), "unit": "elements/s",
-               "cores": torch.get_num_threads(), "kind": "port",
+               **info, "kind": "port",
                "sample": f"first {rows} rows: torch-CPU restatement of validate_artifacts.py:15-55, "
                          f"{(t1 - t0) * 1e3:.1f} ms", "matches_gpu": got == want}
     line = {
@@ -354,46 +379,120 @@ def run_audit(args, torch, np) -> int:
     return 0
 
 
-def _cpu_baseline_moe(L, ne, gpu_out, budget_s):
-    """Time the CPU oracle on whole experts of the same layer until the budget
-    is spent; also report code agreement with the GPU on those experts."""
+def _cpu_setup(torch) -> dict:
+    """CPU leg threads and host description: one
+    thread per core of this process's affinity, capped at the host share the
+    box grants (OMP_NUM_THREADS); the CPU model and the torch build."""
+    aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or aff
+    threads = max(1, min(aff, share))
+    torch.set_num_threads(threads)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                         model)
+    except OSError:
+        pass
+    return {"cores": threads, "affinity_cores": aff, "cpu_model": model,
+            "torch": torch.__version__, "mkl": bool(torch.backends.mkl.is_available())}
+
+
+def _block_diag_groups(H, groups):
+    """[B, 32k, 32k] with the diagonal 32x32 blocks of H for `groups` (the
+    only part of H an MXFP solve reads, gptq.py:99)."""
+    import torch
+
+    k = len(groups)
+    out = torch.zeros(H.shape[0], 32 * k, 32 * k, dtype=torch.float32)
+    for i, g in enumerate(groups):
+        out[:, 32 * i:32 * i + 32, 32 * i:32 * i + 32] = H[:, 32 * g:32 * g + 32, 32 * g:32 * g + 32].cpu()
+    return out
+
+
+def _cpu_baseline_moe(L, ne, gpu_out, budget_s, H_gpu):
+    """The reference's path on the host CPU (the oracle: a torch-CPU
+    restatement of capture.py:68-76, gptq.py and packing.py), in the shape
+    sequential.py:536-626 runs it: per-expert fp32 addmm Hessians, then ONE
+    stacked solve_gptq over all routed experts (the reference's span holds
+    all of them at its default 16 GiB budget), RTN for the unrouted experts
+    and numpy packing.
+
+    Bounded sample, extrapolated linearly: Hessians of whole experts until
+    half the budget is spent (cost per assignment x all assignments), and the
+    stacked solve over every routed expert on a subset of the 32-column
+    groups, which are independent and equal in cost (x groups / sampled
+    groups). RTN and packing are timed in full. Code agreement with the GPU
+    is measured on the sampled groups (the CPU solve gets the GPU's Hessian
+    blocks, so both see identical inputs)."""
+    import numpy as np
     import torch
 
     sys.path.insert(0, ROOT)
-    from oracle import gptq_ref, hessian_ref, packing_ref
+    from oracle import gptq_ref, grid_ref, hessian_ref, packing_ref
 
+    info = _cpu_setup(torch)
     hidden, inter = L.W_gate_up.shape[2], L.W_down.shape[2]
     q_gu, _, q_dn, _, _ = gpu_out
-    spent, done, elems, agree_n, agree_d = 0.0, 0, 0, 0, 0
-    # spread the sample over the expert range (light and heavy experts)
-    order = list(range(0, ne, 7)) + [e for e in range(ne) if e % 7]
-    for e in order:
+    H_gu, H_dn = H_gpu
+    A = L.offsets[ne]
+    # 1. Hessians, whole experts, spread over light and heavy ones
+    spent_h, done_a, n_exp = 0.0, 0, 0
+    for e in list(range(0, ne, 7)) + [e for e in range(ne) if e % 7]:
         a, b = L.offsets[e], L.offsets[e + 1]
         xs = L.X.index_select(0, L.row_index[a:b].long()).cpu()
         ys = L.Y[a:b].cpu()
-        wg = L.W_gate_up[e : e + 1].cpu()
-        wd = L.W_down[e : e + 1].cpu()
         t = time.perf_counter()
-        Hg = hessian_ref.stash_hessian([xs], hidden)
-        Hd = hessian_ref.stash_hessian([ys], inter)
-        rq_g, _, _, _, _ = gptq_ref.solve_gptq(wg, Hg.unsqueeze(0), 4, 32, mode="mxfp4")
-        rq_d, _, _, _, _ = gptq_ref.solve_gptq(wd, Hd.unsqueeze(0), 4, 32, mode="mxfp4")
-        packing_ref.pack_q(rq_g.numpy(), 4)
-        packing_ref.pack_q(rq_d.numpy(), 4)
-        spent += time.perf_counter() - t
-        done += 1
-        elems += wg.numel() + wd.numel()
-        agree_n += int((q_gu[e].cpu() == rq_g[0]).sum()) + int((q_dn[e].cpu() == rq_d[0]).sum())
-        agree_d += rq_g.numel() + rq_d.numel()
-        if spent >= budget_s:
+        hessian_ref.stash_hessian([xs], hidden)
+        hessian_ref.stash_hessian([ys], inter)
+        spent_h += time.perf_counter() - t
+        done_a += b - a
+        n_exp += 1
+        if spent_h >= 0.5 * budget_s:
             break
+    hess_s = spent_h * A / max(done_a, 1)
+    # 2. one stacked solve over all routed experts, on sampled groups
+    solve_s, agree_n, agree_d, sampled, partial = 0.0, 0, 0, [], n_exp < ne
+    for name, W, H, q_g in (("gate_up", L.W_gate_up, H_gu, q_gu), ("down", L.W_down, H_dn, q_dn)):
+        G = W.shape[2] // 32
+        per_group, k = 0.0, 0
+        for g in np.random.default_rng(0).permutation(G):
+            cols = slice(32 * g, 32 * g + 32)
+            Wc = W[:ne, :, cols].cpu()
+            Hc = _block_diag_groups(H[:ne], [g])
+            t = time.perf_counter()
+            rq, _, _, _, _ = gptq_ref.solve_gptq(Wc, Hc, 4, 32, mode="mxfp4")
+            per_group += time.perf_counter() - t
+            k += 1
+            agree_n += int((q_g[:, :, cols].cpu() == rq).sum())
+            agree_d += rq.numel()
+            if per_group >= 0.2 * budget_s:
+                break
+        solve_s += per_group * G / k
+        partial = partial or k < G
+        sampled.append(f"{name} {k}/{G} groups")
+    # 3. RTN of the unrouted experts and numpy packing of every code tensor, in full
+    t = time.perf_counter()
+    rq_g, _, _, _ = grid_ref.rtn_quantize_mxfp(L.W_gate_up[ne:].cpu().float(), "mxfp4")
+    rq_d, _, _, _ = grid_ref.rtn_quantize_mxfp(L.W_down[ne:].cpu().float(), "mxfp4")
+    for qq in (q_gu.cpu().numpy(), q_dn.cpu().numpy(), rq_g.numpy(), rq_d.numpy()):
+        packing_ref.pack_q(qq, 4)
+    tail_s = time.perf_counter() - t
+    total = hess_s + solve_s + tail_s
+    elements = L.W_gate_up.numel() + L.W_down.numel()
     return {
-        "value": round(elems / spent, 1),
+        "value": round(elements / total, 1),
         "unit": "elements/s",
-        "cores": torch.get_num_threads(),
+        **info,
         "kind": "port",
-        "sample": f"{done} of {ne} routed experts of the same layer (gate_up + down each): CPU oracle "
-                  f"Hessian (fp32 addmm) + Cholesky + MXFP4 safe-search GPTQ + pack, {spent:.1f} s",
+        "extrapolated": partial,
+        "seconds": {"hessians": round(hess_s, 2), "solve": round(solve_s, 2),
+                    "rtn_and_pack": round(tail_s, 2), "layer": round(total, 2)},
+        "sample": (f"Hessians of {n_exp}/{ne} routed experts ({done_a}/{A} assignments, fp32 addmm "
+                   f"over 65536-row chunks) x {A / max(done_a, 1):.2f}; one stacked MXFP4 "
+                   f"safe-search solve of all {ne} routed experts on {', '.join(sampled)} (groups "
+                   f"are independent, equal cost), scaled to all groups; RTN of the {L.experts - ne} "
+                   f"unrouted experts and numpy pack_q of the whole layer timed in full"),
         "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
     }
 
@@ -487,6 +586,7 @@ def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
     sys.path.insert(0, ROOT)
     from oracle import gptq_ref, hessian_ref, packing_ref
 
+    info = _cpu_setup(torch)
     res, _ = gpu_out
     t_total, agree_n, agree_d, parts = 0.0, 0, 0, []
     per_budget = budget_s / (len(L.inputs) + len(L.mats))
@@ -521,8 +621,9 @@ def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
     return {
         "value": round(L.elements / t_total, 1),
         "unit": "elements/s",
-        "cores": torch.get_num_threads(),
+        **info,
         "kind": "port",
+        "extrapolated": True,
         "sample": "CPU oracle, extrapolated linearly from " + "; ".join(parts)
                   + f" (estimated {t_total:.1f} s per layer)",
         "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),

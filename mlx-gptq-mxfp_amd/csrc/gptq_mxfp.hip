@@ -40,6 +40,7 @@ namespace {
 
 constexpr int kG = 32;
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kMaxOffsets = 8;
 
 struct Offsets {
@@ -339,9 +340,19 @@ __global__ void __launch_bounds__(kThreads)
   static_assert(!XERR || (SAFE && sizeof(TIn) == 2 && !IS_F16), "XERR needs bf16 weights");
   const int64_t G = C / kG;
   const int64_t chunks = (R + kThreads - 1) / kThreads;
-  const int64_t bg = blockIdx.x / chunks;
-  const int64_t chunk = blockIdx.x % chunks;
-  const int64_t b = bg / G, g = bg % G;
+  // Work order: the group index is fastest, so the workgroups of groups
+  // g, g+1, ... of the same rows are neighbours; and neighbours run on one
+  // XCD: physical block p goes to XCD p % 8, so each XCD is given one
+  // contiguous range of the work order. Two neighbouring groups share every
+  // 128-byte line of W (bf16) and four share every line of q, which are then
+  // fetched and written through one L2 instead of two.
+  const int64_t n_blocks = static_cast<int64_t>(gridDim.x);
+  const int64_t xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+  const int64_t per = n_blocks / kXcds, extra = n_blocks % kXcds;
+  const int64_t work = xcd * per + (xcd < extra ? xcd : extra) + slot;
+  const int64_t g = work % G;
+  const int64_t bc = work / G;
+  const int64_t b = bc / chunks, chunk = bc % chunks;
   const int64_t r_raw = chunk * kThreads + threadIdx.x;
   const bool valid = r_raw < R;
   const int64_t r = valid ? r_raw : R - 1;
