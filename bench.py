@@ -509,16 +509,24 @@ def run_dense(args, torch, np) -> int:
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
     keys = list(L.inputs)
-    Hs = {k: torch.empty(1, X.shape[1], X.shape[1], dtype=torch.float32, device=dev)
-          for k, X in L.inputs.items()}
+    # the drop-in path: each input's rows in a capture.Stash (the reference's
+    # per-matrix stash, capture.py:33-79), its H from Stash.hessian
+    stashes = {}
+    for k in keys:
+        st = capture.Stash(k, L.inputs[k].shape[1])
+        st.add(L.inputs[k])
+        L.inputs[k] = st.chunks[0]  # the stash's copy; the generated one is freed
+        stashes[k] = st
+    torch.cuda.synchronize()
     n_ev = len(keys) + len(L.mats) + 1
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
 
     def step():
         i = 0
         evs[i].record()
+        Hs = {}
         for k in keys:
-            capture.hessian_xtx(L.inputs[k], out=Hs[k][0])
+            Hs[k] = stashes[k].hessian(dev).unsqueeze(0)
             i += 1
             evs[i].record()
         res = []
@@ -529,7 +537,7 @@ def run_dense(args, torch, np) -> int:
         packed = [packing.pack_q(r[0], m.pack_bits) for r, m in zip(res, L.mats)]
         i += 1
         evs[i].record()
-        return (res, packed), evs
+        return (res, packed, Hs), evs
 
     _copy_calibration(torch, dev, args.copy_calib_mib)
     out, ms_step, phase = _timed(torch, np, step, n_ev, args.warmup, args.steps)
@@ -566,7 +574,7 @@ def run_dense(args, torch, np) -> int:
     if dom.startswith("hessian_"):
         # the profile's largest SYRK dispatch is the dominant Hessian
         rooflines[dom]["traffic"] = _traffic(tag, "mgq::syrk_kernel<false")
-    cpu = _cpu_baseline_dense(L, out, Hs, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = _cpu_baseline_dense(L, out[:2], out[2], args.cpu_seconds) if args.cpu_seconds > 0 else None
     config = {"workload": L.name, "elements": elements,
               "matrices": {m.name: list(m.W.shape[1:]) for m in L.mats},
               "tokens": {k: int(X.shape[0]) for k, X in L.inputs.items()}}
