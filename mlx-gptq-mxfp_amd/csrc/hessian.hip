@@ -8,9 +8,9 @@
 // output tiles is computed; each tile is mirrored on store, so H is exactly
 // symmetric.
 //
-// Tile kernel (256 threads = 4 waves, 1 workgroup per CU):
-//   - output tile 256x256, each wave 128x128 = 4x4 blocks of
-//     v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane, in AGPRs);
+// Tile kernel (512 threads = 8 waves, two per SIMD, 1 workgroup per CU):
+//   - output tile 256x256, each wave 128x64 = 4x2 blocks of
+//     v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane);
 //   - token rows are copied HBM -> LDS by global_load_lds_dwordx4 (no VGPR
 //     staging); MFMA operands are read with ds_read_b64_tr_b16 transposing
 //     loads from the token-major LDS rows (see syrk_kernel);
@@ -39,7 +39,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kTile = 256;
 constexpr int kKs = 64;          // token granularity of work-item ranges
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // SYRK workgroup: 8 waves
 constexpr int64_t kMaxItemTokens = 262144;  // longest fp32 accumulation chain per item
 constexpr int kXcds = 8;
 constexpr int kCUs = 256;
@@ -80,7 +80,8 @@ inline int64_t zero_row_bytes(int64_t C) { return align_up(2 * C); }
 // 32-bit (C*C < 2^31 is checked on the host) and the stride is kept in a
 // VGPR so the 64 row offsets are formed per element instead of occupying
 // scalar registers.
-__device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uint32_t ld_s,
+template <int NA>
+__device__ inline void flush(f32x16_t (&acc)[4][NA], float* __restrict__ out, uint32_t ld_s,
                              bool direct, bool add, uint32_t C, uint32_t gi0, uint32_t gj0,
                              int lane, bool interior) {
   uint32_t ld;
@@ -97,7 +98,7 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
       for (int rq = 0; rq < 4; ++rq) {
         const uint32_t gi = gi_l + ma * 32 + 8 * rq;
 #pragma unroll
-        for (int na = 0; na < 4; ++na) {
+        for (int na = 0; na < NA; ++na) {
           const uint32_t gj = gj_l + na * 32;
           float nv[4];
 #pragma unroll
@@ -121,7 +122,7 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
       const uint32_t gi = gi_l + ma * 32 + 8 * (r >> 2) + (r & 3);
       const uint32_t row_off = gi * ld;
 #pragma unroll
-      for (int na = 0; na < 4; ++na) {
+      for (int na = 0; na < NA; ++na) {
         const uint32_t gj = gj_l + na * 32;
         const float v = acc[ma][na][r];
         if (direct) {
@@ -151,8 +152,8 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
 //   - dense: saddr = the stage's first row of this wave, offset = lane chunk
 //     + i * row pitch (fixed per lane);
 //   - gathered, X < 4 GB: saddr = X, offset = row_index[t] * pitch + lane
-//     chunk (one v_readlane + multiply-add per token; the wave's 16 indices
-//     of a stage arrive in one vector load two stages ahead);
+//     chunk (one v_readlane + multiply-add per token; the wave's KB / 8
+//     indices of a stage arrive in one vector load a stage ahead);
 //   - gathered, X >= 4 GB (BIG): saddr = X + row * pitch per token.
 // Tokens past the item's range read a zero row.
 //
@@ -164,15 +165,16 @@ __device__ inline void flush(f32x16_t (&acc)[4][4], float* __restrict__ out, uin
 // transposed read takes from each of its 8 token rows land on four distinct
 // 64-byte bank groups (no conflicts).
 //
-// Schedule of one stage s (nks = KB/16 K-steps of 16 MFMAs, 4x4 blocks of
-// the wave's 128x128 tile): segment k (k = 1..nks-1) runs the 16 MFMAs of
-// K-step k-1, each followed by its share of the fragment reads of K-step k.
-// Then the stage barrier (this wave's DMA of stage s+1 done: vmcnt; every
-// wave done reading stage s: lgkmcnt(0) before s_barrier), after which
-// segment 0 of stage s+1 runs the last K-step's MFMAs of stage s together
-// with the first fragment reads of stage s+1 and the DMA of stage s+NB into
-// the buffer stage s just released. Fragments are double-buffered in VGPRs
-// (fa/fb[2][4]); each MFMA is fenced by sched_barrier so this order is kept.
+// Schedule of one stage s (nks = KB/16 K-steps of 8 MFMAs, the 4x2 blocks
+// of the wave's 128x64 part): segment k (k = 1..nks-1) runs the 8 MFMAs of
+// K-step k-1, the first six each followed by one of the six fragment reads
+// (a0 b0 b1 a1 a2 a3) of K-step k. Then the stage barrier (this wave's DMA
+// of stage s+1 done: vmcnt; every wave done reading stage s: lgkmcnt(0)
+// before s_barrier), after which segment 0 of stage s+1 runs the last
+// K-step's MFMAs of stage s together with the first fragment reads of stage
+// s+1 and the DMA of stage s+NB into the buffer stage s just released.
+// Fragments are double-buffered in VGPRs (fa[2][4], fb[2][2]); each MFMA is
+// fenced by sched_barrier so this order is kept.
 __device__ inline void dma_tok(uint32_t lds_dst, uint32_t voffset, const char* saddr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
@@ -193,35 +195,41 @@ __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-#define SYRK_MFMA(P, j)                                                                    \
-  acc[(j) >> 2][(j) & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                        \
-      fa[P][(j) >> 2], fb[P][(j) & 3], acc[(j) >> 2][(j) & 3], 0, 0, 0)
-// fragment q of a K-step, in the order the MFMAs consume them: a0 b0 b1 b2 b3 a1 a2 a3
-#define SYRK_READ(P, q, b)                                                                 \
+// Waves: eight per workgroup, two per SIMD. Wave (wr, wc) = (w / 4, w % 4)
+// owns rows 128 wr .. +128 and columns 64 wc .. +64 of the tile (4 x 2
+// blocks, 128 fp32 accumulators per lane) and issues KB / 8 of a stage's
+// DMAs. With two waves on a SIMD, the issue stall of one wave's DMA (the TA
+// accepts a 1 KB request per ~16 cycles) leaves the matrix pipe to the other
+// wave's MFMAs; with one wave per SIMD (a 128x128 quarter each) the same
+// stall idled the pipe (measured 3-6 % slower, same results bit for bit).
+#define SYRK_MFMA(P, j)                                                                   \
+  acc[(j) >> 1][(j) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                        \
+      fa[P][(j) >> 1], fb[P][(j) & 1], acc[(j) >> 1][(j) & 1], 0, 0, 0)
+// fragment q of a K-step, in the order the MFMAs consume them: a0 b0 b1 a1 a2 a3
+#define SYRK_READ(P, q, b)                                                                \
   do {                                                                                     \
     if ((q) == 0)                                                                          \
       fa[P][0] = tr_frag(lds3 + (b) + offA[0]);                                            \
-    else if ((q) <= 4)                                                                     \
+    else if ((q) <= 2)                                                                     \
       fb[P][(q) - 1] = tr_frag(lds3 + (b) + offB[(q) - 1]);                                \
     else                                                                                   \
-      fa[P][(q) - 4] = tr_frag(lds3 + (b) + offA[(q) - 4]);                                \
+      fa[P][(q) - 2] = tr_frag(lds3 + (b) + offA[(q) - 2]);                                \
   } while (0)
 
 template <bool GATHER, bool BIG, int KB, int NB>
 __global__ void __launch_bounds__(kThreads, 1)
     syrk_kernel(const uint16_t* __restrict__ X, int64_t n_rows, int64_t ldx, int64_t C,
-                const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
-                float* __restrict__ H, float* __restrict__ partials, int accumulate,
-                const uint16_t* __restrict__ zero_row) {
-  constexpr int kDmaWave = KB / 4;  // tokens (= DMA instructions) per wave and stage
+                 const int32_t* __restrict__ row_index, const HessItem* __restrict__ items,
+                 float* __restrict__ H, float* __restrict__ partials, int accumulate,
+                 const uint16_t* __restrict__ zero_row) {
+  constexpr int kDmaWave = KB / 8;  // tokens (= DMA instructions) per wave and stage
   constexpr int kStageB = KB * kTokB;
   constexpr int nks = KB / 16;
   constexpr int L = (nks - 1) & 1;  // fragment buffer of a stage's last K-step
-  constexpr int kDmaEvery = 16 / kDmaWave;
-  static_assert(KB % 32 == 0 && kDmaWave <= 16, "stage shape");
+  constexpr int kDmaEvery = 8 / kDmaWave;  // one DMA every kDmaEvery MFMAs of segment 0
+  static_assert(KB % 32 == 0 && kDmaWave <= 8 && (kDmaWave & (kDmaWave - 1)) == 0, "stage shape");
   static_assert(NB * kStageB <= 160 * 1024, "LDS budget");
   static_assert(!GATHER || NB == 2, "gathered row indices are loaded one stage ahead");
-  // stage barrier: vmcnt(DMA stages still allowed in flight), lgkmcnt(0)
   constexpr int kVm = (NB - 2) * kDmaWave;
   static_assert(kVm <= 63, "vmcnt range");
   constexpr int kWait = (kVm & 15) | ((kVm >> 4) << 14) | (7 << 4);
@@ -232,18 +240,15 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave >> 2, wc = wave & 3;
   const bool diag = it.ti == it.tj;
   const bool direct = it.slot < 0;
   float* out = direct ? H + static_cast<int64_t>(it.g) * C * C
                       : partials + static_cast<int64_t>(it.slot) * kTile * kTile;
   const uint32_t ld = direct ? static_cast<uint32_t>(C) : kTile;
   const uint32_t gi0 = (direct ? static_cast<uint32_t>(it.ti) * kTile : 0u) + wr * 128;
-  const uint32_t gj0 = (direct ? static_cast<uint32_t>(it.tj) * kTile : 0u) + wc * 128;
+  const uint32_t gj0 = (direct ? static_cast<uint32_t>(it.tj) * kTile : 0u) + wc * 64;
 
-  // DMA lane role: slot (lane & 31) of the A (lane < 32) or B half of LDS
-  // token row t holds chunk slot ^ 4*(t & 3); channels past C are clamped (they
-  // only feed output rows / columns >= C, which are never stored).
   const int half = lane >> 5;
   const int64_t tile_ch = static_cast<int64_t>(half && !diag ? it.tj : it.ti) * kTile;
   uint32_t voff[4];
@@ -252,26 +257,23 @@ __global__ void __launch_bounds__(kThreads, 1)
     const int64_t ch = tile_ch + 8 * ((lane & 31) ^ (4 * f));
     voff[f] = static_cast<uint32_t>(2 * (ch < C - 8 ? ch : C - 8));
   }
-  // Transposed-read lane role: group g = lane/16, source j = (lane/4)%4, q = lane%4.
-  // Source j reads LDS token row 4r + j (+ 8, 16 multiples), so its swizzle is j.
   const int g = lane >> 4, j4 = (lane >> 2) & 3, q = lane & 3;
   const uint32_t rd_lo = static_cast<uint32_t>((8 * (g >> 1) + j4) * kTokB + (g & 1) * 32 +
                                                (q >> 1) * 16 + (q & 1) * 8);
-  uint32_t offA[4], offB[4];
+  uint32_t offA[4], offB[2];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    offA[m] = rd_lo + wr * 256 + (m ^ j4) * 64;
-    offB[m] = rd_lo + 512 + wc * 256 + (m ^ j4) * 64;
-  }
+  for (int m = 0; m < 4; ++m) offA[m] = rd_lo + wr * 256 + (m ^ j4) * 64;
+#pragma unroll
+  for (int n = 0; n < 2; ++n) offB[n] = rd_lo + 512 + ((2 * wc + n) ^ j4) * 64;
   const lds_char_t* lds3 = (const lds_char_t*)lds;
   const uint32_t lds_u32 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds3));
   const uint32_t wave_dst = wave * kDmaWave * kTokB;
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[4][2];
 #pragma unroll
   for (int ma = 0; ma < 4; ++ma)
 #pragma unroll
-    for (int na = 0; na < 4; ++na)
+    for (int na = 0; na < 2; ++na)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[ma][na][r] = 0.0f;
 
@@ -281,13 +283,11 @@ __global__ void __launch_bounds__(kThreads, 1)
   const uint32_t nr1 = static_cast<uint32_t>(n_rows - 1);
   const int64_t k0 = it.k0, k1 = it.k1;
   const int n_stages = static_cast<int>((k1 - k0 + KB - 1) / KB);
-  const int64_t twave = k0 + wave * kDmaWave;  // this wave's first token of stage 0
+  const int64_t twave = k0 + wave * kDmaWave;
   uint32_t vofs[kDmaWave];
 #pragma unroll
   for (int i = 0; i < kDmaWave; ++i) vofs[i] = voff[i & 3] + i * ldx2;
 
-  // Row indices of this wave's tokens of the stage starting at t0: lane i
-  // (i < kDmaWave) holds token t0 + i, clamped into the item's range.
   auto load_idx = [&](int64_t t0) -> int32_t {
     if constexpr (GATHER) {
       const int64_t t = t0 + (lane & (kDmaWave - 1));
@@ -296,13 +296,12 @@ __global__ void __launch_bounds__(kThreads, 1)
       return 0;
     }
   };
-  // DMA of token i of this wave's share of a stage (rem tokens are in range).
   auto dma_i = [&](int i, uint32_t dst, int rem, int32_t idxv, const char* base) {
     const char* sa;
     uint32_t vo;
     if constexpr (GATHER) {
       uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(idxv, i));
-      r = r < nr1 ? r : nr1;  // a bad index is clamped, never dereferenced
+      r = r < nr1 ? r : nr1;
       if constexpr (BIG) {
         sa = Xb + static_cast<uint64_t>(r) * ldx2;
         vo = voff[i & 3];
@@ -326,8 +325,7 @@ __global__ void __launch_bounds__(kThreads, 1)
   };
 
   if (n_stages > 0) {
-    bf16x8_t fa[2][4], fb[2][4];
-    // prologue: stages 0 .. NB-2 in flight, barrier, first fragments, stage NB-1
+    bf16x8_t fa[2][4], fb[2][2];
 #pragma unroll
     for (int p = 0; p < NB - 1; ++p) {
       const int64_t t0 = twave + p * KB;
@@ -341,9 +339,8 @@ __global__ void __launch_bounds__(kThreads, 1)
     __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int qq = 0; qq < 8; ++qq) SYRK_READ(0, qq, 0u);
+    for (int qq = 0; qq < 6; ++qq) SYRK_READ(0, qq, 0u);
     {
-      // stages past the item's range load zero rows (their buffers are never read)
       const int64_t t0 = twave + (NB - 1) * KB;
       const int rem = stage_rem(t0);
       const char* base = stage_base(t0);
@@ -359,15 +356,15 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int ks = 1; ks < nks; ++ks) {
         const int P = (ks - 1) & 1;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < 8; ++j) {
           SYRK_MFMA(P, j);
-          if ((j & 1) == 0) SYRK_READ(P ^ 1, j >> 1, rd + ks * 16 * kTokB);
+          if (j < 6) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
           if (GATHER && ks == 1 && j == 1)
             idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      const uint32_t wbuf = static_cast<uint32_t>(rbuf);  // stage s's buffer takes stage s+NB
+      const uint32_t wbuf = static_cast<uint32_t>(rbuf);
       rbuf = rbuf + 1 == NB ? 0 : rbuf + 1;
       __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
       __builtin_amdgcn_s_barrier();
@@ -379,9 +376,9 @@ __global__ void __launch_bounds__(kThreads, 1)
       const char* base = stage_base(t0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < 8; ++j) {
         SYRK_MFMA(L, j);
-        if ((j & 1) == 0) SYRK_READ(L ^ 1, j >> 1, nrd);
+        if (j < 6) SYRK_READ(L ^ 1, j, nrd);
         if (j % kDmaEvery == kDmaEvery - 1) dma_i(j / kDmaEvery, dst, rem, idx_n, base);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -392,22 +389,21 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int ks = 1; ks < nks; ++ks) {
         const int P = (ks - 1) & 1;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < 8; ++j) {
           SYRK_MFMA(P, j);
-          if ((j & 1) == 0) SYRK_READ(P ^ 1, j >> 1, rd + ks * 16 * kTokB);
+          if (j < 6) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) SYRK_MFMA(L, j);
+      for (int j = 0; j < 8; ++j) SYRK_MFMA(L, j);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the trailing (zero-row) stages' DMA
+    __builtin_amdgcn_s_waitcnt(0);
   }
-  // Empty ranges (n_stages == 0) still flush, so an unrouted group gets H = 0.
   const bool interior =
       direct && it.ti > it.tj && (static_cast<int64_t>(it.ti) + 1) * kTile <= C;
-  flush(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
-        interior);
+  flush<2>(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
+           interior);
 }
 #undef SYRK_MFMA
 #undef SYRK_READ
