@@ -189,3 +189,43 @@ def test_reference_checkout_resolves_the_other_modules(tmp_path):
                          timeout=300)
     assert out.returncode == 0, out.stderr
     assert out.stdout.strip() == "ok"
+
+
+def test_capture_manager_backfill_and_fallback_keys():
+    """Never-routed experts are backfilled through the manager
+    (capture.py:254-322) and reported under the reference's stash keys."""
+    from mlx_gptq import capture
+
+    layer = _toy_layer()
+    blk = layer.mlp
+    gate_fwd = blk.gate.forward
+
+    def never_three(h):  # the router never picks expert 3
+        logits, _, _ = gate_fwd(h)
+        masked = logits.clone()
+        masked[:, 3] = -float("inf")
+        probs = torch.softmax(masked, dim=-1, dtype=torch.float)
+        vals, idx = torch.topk(probs, 2, dim=-1)
+        return logits, (vals / vals.sum(-1, keepdim=True)).to(logits.dtype), idx
+
+    blk.gate.forward = never_three
+    layer.forward = lambda x: blk(layer.self_attn.q_proj(x))
+    mgr = capture.CaptureManager(layer, None, 32)
+    g = torch.Generator().manual_seed(0)
+    with torch.no_grad(), mgr:
+        for _ in range(2):
+            mgr.begin_batch()
+            layer(torch.randn(1, 40, 64, generator=g))
+    mgr.check_capture_happened()
+    assert mgr.stashes["mlp.experts.gate_up_proj::e3"].tokens == 0
+    zero = [e for e in range(4) if mgr.stashes[f"mlp.experts.gate_up_proj::e{e}"].tokens == 0]
+    assert 3 in zero and mgr.expert_token_stats()["mlp.experts.gate_up_proj"][3] == len(zero)
+    assert mgr.backfill_unrouted_experts() == {"mlp.experts": zero}
+    assert mgr.fallback_experts == {f"mlp.experts.{p}::e{e}": "all_expert_inputs"
+                                    for e in zero for p in ("gate_up_proj", "down_proj")}
+    # the block's sampled inputs (64 evenly spaced rows of each 40-row batch: all of them)
+    assert mgr.stashes["mlp.experts.gate_up_proj::e3"].tokens == 80
+    assert mgr.stashes["mlp.experts.down_proj::e3"].tokens == 80
+    assert mgr.stashes["self_attn.q_proj"].tokens == 80
+    mgr.drop_all()
+    assert mgr.total_stash_bytes() == 0
