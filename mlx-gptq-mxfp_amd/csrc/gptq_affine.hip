@@ -15,6 +15,8 @@
 // After the block a separate kernel applies the deferred update
 //     W[:, i2:] -= Err @ U[i1:i2, i2:]
 // (the reference's bmm) as an fp32 GEMM.
+#include <type_traits>
+
 #include "mgq_capi.h"
 #include "mgq_common.h"
 #include "mx_hw.h"
@@ -36,23 +38,116 @@ struct Shrinks {
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 __device__ inline float nan_min(float m, float a) { return (a < m || a != a) ? a : m; }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+// ---- cross-lane steps without LDS traffic --------------------------------
+// A butterfly over the xor masks 32, 16, 8, 4, 2, 1 (in that order). xor 32
+// and xor 16 go through gfx950's v_permlane32_swap / v_permlane16_swap: with
+// both operands v, the swap leaves ([lo | lo], [hi | hi]) for 32 and (rows
+// [r0 r0 r2 r2], [r1 r1 r3 r3]) for 16, so a lane's partner is one of the two
+// results. xor 8 is a DPP rotation by 8 inside each 16-lane row. xor 2 and
+// xor 1 are DPP quad permutations.
+template <int CTRL>
+__device__ inline float dpp_read(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4e, kDppXor1 = 0xb1;
+
+__device__ inline float2 swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ inline float2 swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
+// N sums in one butterfly: v[i] <- v[i] + partner at every step, the
+// rounding of an xor butterfly with __shfl_xor. Because a + b == b + a,
+// both lanes of a pair hold the same bits after each step: the xor-32/16
+// sums are lo + hi in every lane, and after the 8 step a lane's value
+// depends only on lane mod 8, so a rotation by 4 reads the value of lane ^ 4.
+template <int N>
+__device__ inline void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float2 s = swap32(v[i]);
+    v[i] = s.x + s.y;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float2 s = swap16(v[i]);
+    v[i] = s.x + s.y;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppRor8>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppRor4>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppXor2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppXor1>(v[i]);
+}
+
+// wave_nan_min and wave_nan_max of two values in one xor butterfly, each
+// lane applying f(own, partner). nan_min / nan_max are not symmetric in the
+// sign of a zero, so every step reads the exact xor partner (xor 4 through
+// __shfl_xor).
+__device__ inline void wave_nan_minmax(float& lo, float& hi, int lane) {
+  const bool lo32 = lane < 32, even16 = (lane & 16) == 0;
+  {
+    const float2 a = swap32(lo), b = swap32(hi);
+    lo = nan_min(lo, lo32 ? a.y : a.x);
+    hi = nan_max(hi, lo32 ? b.y : b.x);
+  }
+  {
+    const float2 a = swap16(lo), b = swap16(hi);
+    lo = nan_min(lo, even16 ? a.y : a.x);
+    hi = nan_max(hi, even16 ? b.y : b.x);
+  }
+  {
+    const float a = dpp_read<kDppRor8>(lo), b = dpp_read<kDppRor8>(hi);
+    lo = nan_min(lo, a);
+    hi = nan_max(hi, b);
+  }
+  {
+    const float a = __shfl_xor(lo, 4), b = __shfl_xor(hi, 4);
+    lo = nan_min(lo, a);
+    hi = nan_max(hi, b);
+  }
+  {
+    const float a = dpp_read<kDppXor2>(lo), b = dpp_read<kDppXor2>(hi);
+    lo = nan_min(lo, a);
+    hi = nan_max(hi, b);
+  }
+  {
+    const float a = dpp_read<kDppXor1>(lo), b = dpp_read<kDppXor1>(hi);
+    lo = nan_min(lo, a);
+    hi = nan_max(hi, b);
+  }
+}
+
+// ---- exact division by a positive divisor ----------------------------------
 // a / d for d > 0 (or NaN), correctly rounded: Markstein's correction from
 // y = div_exact_recip(d) (mx_hw.h); a zero numerator is returned as is (a / d
 // keeps its sign for d > 0); outside the correction's range the IEEE
 // division. Every divisor here is positive: the clip scale (range >= 0) and
-// U's diagonal.
-__device__ inline float div_pos(float a, float d, float y) {
+// U's diagonal. div_fast is the correction, div_slow says when it is not
+// exact (the operators are the non-short-circuit ones so that no branch is
+// formed around the test).
+__device__ inline float div_fast(float a, float d, float y) {
   const float q = a * y;
   const float r = fmaf(-q, d, a);
-  float e = fmaf(r, y, q);
+  return fmaf(r, y, q);
+}
+__device__ inline bool div_slow(float a, float y) {
   const uint32_t ea = f2u(a) & 0x7f800000u;
-  const bool slow = a != 0.0f && (!(y != 0.0f) || (ea - (27u << 23)) > (200u << 23));
+  return (a != 0.0f) & ((!(y != 0.0f)) | ((ea - (27u << 23)) > (200u << 23)));
+}
+
+__device__ inline float div_pos(float a, float d, float y) {
+  float e = div_fast(a, d, y);
+  const bool slow = div_slow(a, y);
   // the IEEE division only when some lane needs it: a wave-uniform branch
   // (the empty asm keeps the compiler from hoisting the division out of it)
   if (__builtin_amdgcn_ballot_w64(slow) != 0) {
@@ -63,11 +158,16 @@ __device__ inline float div_pos(float a, float d, float y) {
   return a == 0.0f ? a : e;
 }
 
+// grid.py:215-221 from a quotient (w - b) / s_safe: q = clamp(rne(quot), 0,
+// maxq), NaN kept
+__device__ inline float affine_round(float quot, float maxq) {
+  const float q = rintf(quot);
+  return q != q ? q : fminf(fmaxf(q, 0.0f), maxq);
+}
+
 // grid.py:215-221: q = clamp(rne((w - b) / s_safe), 0, maxq); ys = RN(1/s_safe)
 __device__ inline float affine_q(float w, float b, float s_safe, float ys, float maxq) {
-  float q = rintf(div_pos(w - b, s_safe, ys));
-  if (q != q) return q;
-  return fminf(fmaxf(q, 0.0f), maxq);
+  return affine_round(div_pos(w - b, s_safe, ys), maxq);
 }
 
 // gptq.py:216-222 for the affine path: dead columns zeroed in W, H diag := 1.
@@ -91,47 +191,24 @@ __global__ void dead_fix_h_kernel(float* __restrict__ H, int64_t B, int64_t C) {
   }
 }
 
-// N shrink candidates' error sums reduced together: the same butterfly (and
-// so the same rounding) as wave_sum, with the shuffle latencies of the N
-// chains overlapped.
-template <int N>
-__device__ inline void wave_sum_n(float (&v)[N]) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float t[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], off);
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += t[i];
-  }
-}
-
-// wave_nan_min and wave_nan_max of two values in one butterfly
-__device__ inline void wave_nan_minmax(float& lo, float& hi) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float a = __shfl_xor(lo, off), b = __shfl_xor(hi, off);
-    lo = nan_min(lo, a);
-    hi = nan_max(hi, b);
-  }
-}
-
-// Row k of U restricted to the group's columns: lane t holds U[k][j + t + 64 s].
-// LDSU: from the block's copy Ublk[(k - i1) * n + (col - i1)] in LDS, else
-// from global memory.
+// Row k of U restricted to the group's columns: lane t holds U[k][j + t + 64 s]
+// (0 past the group). LDSU: from the block's copy Ublk[(k - i1) * n + (col -
+// i1)] in LDS, else from global memory. Lanes past the group read the
+// group's first column, so the load needs no branch.
 template <int CPL, bool LDSU>
 __device__ inline void load_urow(const float* __restrict__ Ub, const float* Ublk, int64_t C,
                                  int64_t i1, int n, int64_t k, int64_t j, int lane,
                                  const bool (&act)[CPL], float (&u)[CPL]) {
-  if constexpr (LDSU) {
-    const float* Uk = Ublk + (k - i1) * n + (j - i1);
+  const float* Uk = LDSU ? Ublk + (k - i1) * n + (j - i1) : Ub + k * C + j;
 #pragma unroll
-    for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
-  } else {
-    const float* Uk = Ub + k * C + j;
-#pragma unroll
-    for (int s = 0; s < CPL; ++s) u[s] = act[s] ? Uk[lane + 64 * s] : 0.0f;
+  for (int s = 0; s < CPL; ++s) {
+    const float v = Uk[act[s] ? lane + 64 * s : 0];
+    u[s] = act[s] ? v : 0.0f;
   }
+}
+
+__device__ inline float lane_read(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
 // Grid (ceil(R / 4), B): the four waves of a workgroup take rows of one
@@ -197,7 +274,8 @@ __global__ void __launch_bounds__(kWaves * 64)
       act[s] = col < G;
       acc[s] = act[s] ? Wr[j + col] : 0.0f;
       // U's diagonal of the lane's column and its reciprocal for div_pos
-      dg[s] = act[s] ? Ub[(j + col) * C + j + col] : 1.0f;
+      const int cc = act[s] ? col : 0;
+      dg[s] = act[s] ? (LDSU ? Ublk[(j - i1 + cc) * (n + 1)] : Ub[(j + cc) * (C + 1)]) : 1.0f;
       yd[s] = div_exact_recip(dg[s]);
     }
     // earlier in-block updates, in column order; sixteen rows of U in flight
@@ -212,8 +290,7 @@ __global__ void __launch_bounds__(kWaves * 64)
         for (int t = 0; t < 16; ++t) {
           const float e = errs[k + t];
 #pragma unroll
-          for (int s = 0; s < CPL; ++s)
-            if (act[s]) acc[s] = acc[s] - e * u[t][s];
+          for (int s = 0; s < CPL; ++s) acc[s] = act[s] ? acc[s] - e * u[t][s] : acc[s];
         }
       }
       for (; k < kn; ++k) {
@@ -221,8 +298,7 @@ __global__ void __launch_bounds__(kWaves * 64)
         load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, i1 + k, j, lane, act, u);
         const float e = errs[k];
 #pragma unroll
-        for (int s = 0; s < CPL; ++s)
-          if (act[s]) acc[s] = acc[s] - e * u[s];
+        for (int s = 0; s < CPL; ++s) acc[s] = act[s] ? acc[s] - e * u[s] : acc[s];
       }
     }
     // clip search (grid.py:167-212) on the group's current values
@@ -234,7 +310,7 @@ __global__ void __launch_bounds__(kWaves * 64)
         lo = nan_min(lo, acc[s]);
         hi = nan_max(hi, acc[s]);
       }
-    wave_nan_minmax(lo, hi);
+    wave_nan_minmax(lo, hi, lane);
     const float wmin = lo, wmax = hi;
     const float range = wmax - wmin;
     float best_err = 0.0f, s32 = 0.0f, b32 = 0.0f;
@@ -247,24 +323,45 @@ __global__ void __launch_bounds__(kWaves * 64)
       const float ys_l = div_exact_recip(ss_l);
       // candidates kCand at a time, their error sums reduced in one
       // butterfly; slots past the batch score a copy of its last candidate
-      // (an equal error never replaces the earlier best under strict '<')
+      // (an equal error never replaces the earlier best under strict '<').
+      // The quotients of the whole batch take the exact-division correction,
+      // with one wave-uniform test for the rare operands outside its range.
       const int nb = sh.n - 64 * bt < 64 ? sh.n - 64 * bt : 64;
       for (int c0 = 0; c0 < nb; c0 += kCand) {
-        float sc[kCand], bi[kCand], part[kCand];
+        float sc[kCand], bi[kCand], ss[kCand], ys[kCand], part[kCand];
+        float num[kCand][CPL], quo[kCand][CPL];
+        bool slow = false;
 #pragma unroll
         for (int i = 0; i < kCand; ++i) {
           const int ci = c0 + i < nb ? c0 + i : nb - 1;
-          sc[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_l), ci));
-          bi[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bi_l), ci));
-          const float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss_l), ci));
-          const float ys = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ys_l), ci));
+          sc[i] = lane_read(sc_l, ci);
+          bi[i] = lane_read(bi_l, ci);
+          ss[i] = lane_read(ss_l, ci);
+          ys[i] = lane_read(ys_l, ci);
+#pragma unroll
+          for (int s = 0; s < CPL; ++s) {
+            num[i][s] = acc[s] - bi[i];
+            quo[i][s] = div_fast(num[i][s], ss[i], ys[i]);
+            slow |= act[s] & div_slow(num[i][s], ys[i]);
+          }
+        }
+        if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int i = 0; i < kCand; ++i)
+#pragma unroll
+            for (int s = 0; s < CPL; ++s)
+              if (act[s] && div_slow(num[i][s], ys[i])) quo[i][s] = num[i][s] / ss[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kCand; ++i) {
           part[i] = 0.0f;
 #pragma unroll
-          for (int s = 0; s < CPL; ++s)
-            if (act[s]) {
-              const float d = affine_q(acc[s], bi[i], ss, ys, maxq) * sc[i] + bi[i] - acc[s];
-              part[i] += d * d;
-            }
+          for (int s = 0; s < CPL; ++s) {
+            const float qt = num[i][s] == 0.0f ? num[i][s] : quo[i][s];
+            const float d = affine_round(qt, maxq) * sc[i] + bi[i] - acc[s];
+            part[i] = act[s] ? part[i] + d * d : part[i];
+          }
         }
         wave_sum_n<kCand>(part);
 #pragma unroll
@@ -284,69 +381,109 @@ __global__ void __launch_bounds__(kWaves * 64)
     }
     const float s_safe = (fabsf(s32) < 1e-12f) ? 1.0f : s32;
     const float ysafe = div_exact_recip(s_safe);
-    // Sequential columns of the group. The column's value, U's diagonal and
-    // its reciprocal are read from the owner lane (v_readlane, so every lane
-    // computes the same error); the owner lane keeps its code, dequantized
-    // value and error for the group's coalesced stores; U rows arrive eight
-    // columns ahead.
-    float qv[CPL], dqv[CPL], ev[CPL];
+    // Sequential columns of the group. wn is the current column's value: the
+    // owner lane's value after the updates of every earlier column. Before
+    // column c's update the wave reads lane c+1's value (updated through
+    // column c-1) and U[c, c+1], and wn = pre - e * U[c, c+1] repeats lane
+    // c+1's own update (the same two roundings), so no lane read waits for
+    // the column's error. Every lane past c applies w <- w - e * U[c, col]
+    // (lanes past the group too: their values are never read). A column's
+    // lane is not updated after its own column, so at the group's end it
+    // holds the value its column was quantized from.
+    //
+    // The two divisions of a column take Markstein's correction without a
+    // branch (EXACT = false); the operands outside its exact range are only
+    // recorded. If any occurred, the group is run again from its start values
+    // with the guarded division (EXACT = true), so every quotient is the
+    // correctly rounded one either way.
+    float acc0[CPL];
 #pragma unroll
-    for (int s = 0; s < CPL; ++s) qv[s] = dqv[s] = ev[s] = 0.0f;
-    auto column = [&](int c, const float (&uc)[CPL]) __attribute__((always_inline)) {
-      const int owner = c & 63, slot = c >> 6;
-      float mine_v = acc[0], diag_v = dg[0], yd_v = yd[0];
+    for (int s = 0; s < CPL; ++s) acc0[s] = acc[s];
+    auto run_columns = [&](auto exact_tag) __attribute__((always_inline)) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      bool slow = false;
+      float wn = lane_read(acc[0], 0);
+      auto column = [&](int c, const float (&uc)[CPL]) __attribute__((always_inline)) {
+        const int owner = c & 63, slot = c >> 6;
+        const int c1 = c + 1 < G ? c + 1 : c;
+        const int owner1 = c1 & 63, slot1 = c1 >> 6;
+        float diag_v = dg[0], yd_v = yd[0], pre_v = acc[0], u_v = uc[0];
 #pragma unroll
-      for (int s = 1; s < CPL; ++s)
-        if (s == slot) {
-          mine_v = acc[s];
-          diag_v = dg[s];
-          yd_v = yd[s];
+        for (int s = 1; s < CPL; ++s) {
+          if (s == slot) {
+            diag_v = dg[s];
+            yd_v = yd[s];
+          }
+          if (s == slot1) {
+            pre_v = acc[s];
+            u_v = uc[s];
+          }
         }
-      const float mine = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine_v), owner));
-      const float diag = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, diag_v), owner));
-      const float ydg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, yd_v), owner));
-      const float q = affine_q(mine, b32, s_safe, ysafe, maxq);
-      const float dq = q * s32 + b32;
-      const float e = div_pos(mine - dq, diag, ydg);
+        const float diag = lane_read(diag_v, owner), ydg = lane_read(yd_v, owner);
+        const float pre1 = lane_read(pre_v, owner1), u1 = lane_read(u_v, owner1);
+        float e;
+        if constexpr (EXACT) {
+          const float q = affine_q(wn, b32, s_safe, ysafe, maxq);
+          const float dq = q * s32 + b32;
+          e = div_pos(wn - dq, diag, ydg);
+        } else {
+          const float n1 = wn - b32;
+          const float t1 = div_fast(n1, s_safe, ysafe);
+          const float q = affine_round(n1 == 0.0f ? n1 : t1, maxq);
+          const float dq = q * s32 + b32;
+          const float n2 = wn - dq;
+          const float t2 = div_fast(n2, diag, ydg);
+          e = n2 == 0.0f ? n2 : t2;
+          slow |= div_slow(n1, ysafe) | div_slow(n2, ydg);
+        }
 #pragma unroll
-      for (int s = 0; s < CPL; ++s) {
-        const int col = lane + 64 * s;
-        const bool own = col == c;
-        qv[s] = own ? q : qv[s];
-        dqv[s] = own ? dq : dqv[s];
-        ev[s] = own ? e : ev[s];
-        acc[s] = (act[s] && col > c) ? acc[s] - e * uc[s] : acc[s];
+        for (int s = 0; s < CPL; ++s) acc[s] = lane + 64 * s > c ? acc[s] - e * uc[s] : acc[s];
+        wn = pre1 - e * u1;
+      };
+      // U rows arrive eight columns ahead (rows past the group repeat its last)
+      const int G8 = G & ~7;
+      float ring[8][CPL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + (u < G ? u : G - 1), j, lane, act, ring[u]);
+      for (int c0 = 0; c0 < G8; c0 += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int c = c0 + u;
+          float uc[CPL];
+#pragma unroll
+          for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
+          const int nxt = c + 8 < G ? c + 8 : G - 1;
+          load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + nxt, j, lane, act, ring[u]);
+          column(c, uc);
+        }
       }
-    };
-    const int G8 = G & ~7;
-    float ring[8][CPL];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (u < G8) load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + u, j, lane, act, ring[u]);
-    for (int c0 = 0; c0 < G8; c0 += 8) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int c = c0 + u;
+      for (int c = G8; c < G; ++c) {
         float uc[CPL];
-#pragma unroll
-        for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
-        if (c + 8 < G8) load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c + 8, j, lane, act, ring[u]);
+        load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c, j, lane, act, uc);
         column(c, uc);
       }
+      return slow;
+    };
+    // every lane computed the same chain, so `slow` is wave-uniform
+    if (__builtin_amdgcn_ballot_w64(run_columns(std::false_type{})) != 0) {
+#pragma unroll
+      for (int s = 0; s < CPL; ++s) acc[s] = acc0[s];
+      run_columns(std::true_type{});
     }
-    for (int c = G8; c < G; ++c) {
-      float uc[CPL];
-      load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c, j, lane, act, uc);
-      column(c, uc);
-    }
+    // each lane's code, dequantized value and error, from the value its
+    // column was quantized from (the same operations as the column step)
 #pragma unroll
     for (int s = 0; s < CPL; ++s) {
+      const float q = affine_q(acc[s], b32, s_safe, ysafe, maxq);
+      const float dq = q * s32 + b32;
+      const float e = div_pos(acc[s] - dq, dg[s], yd[s]);
       if (!act[s]) continue;
       const int col = lane + 64 * s;
-      q_out[row * C + j + col] = (qv[s] == qv[s]) ? static_cast<uint8_t>(qv[s]) : 0;
-      Wr[j + col] = dqv[s];
-      errs[j + col - i1] = ev[s];
-      Err[row * n + (j + col - i1)] = ev[s];
+      q_out[row * C + j + col] = (q == q) ? static_cast<uint8_t>(q) : 0;
+      Wr[j + col] = dq;
+      errs[j + col - i1] = e;
+      Err[row * n + (j + col - i1)] = e;
     }
     // errs[] is read by every lane of this wave at the next group start
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
