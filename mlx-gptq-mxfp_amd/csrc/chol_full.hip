@@ -229,21 +229,31 @@ __device__ inline void load4(const double* __restrict__ p, int64_t stride, int c
   }
 }
 
+// One product's operands: C = alpha * A opB + beta * C, per batch item.
+struct GemmArgs {
+  const double* A;
+  int64_t lda, sA;
+  const double* B;
+  int64_t ldb, sB;
+  double* C;
+  int64_t ldc, sC;
+  int M, N, K;
+  double alpha, beta;
+};
+
+// The 32 x 32 output tile at (m0, n0) of batch item `item`; red is the
+// workgroup's LDS for the four waves' partial tiles.
 template <bool TRANSB, bool UPPER>
-__global__ void __launch_bounds__(256)
-    dgemm_kernel(const double* __restrict__ A, int64_t lda, int64_t sA,
-                 const double* __restrict__ B, int64_t ldb, int64_t sB, double* __restrict__ Cm,
-                 int64_t ldc, int64_t sC, int M, int N, int K, double alpha, double beta,
-                 const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
-  const int64_t item = blockIdx.z;
-  if (!active[item] || failed[item]) return;
-  const int m0 = blockIdx.y * kMt, n0 = blockIdx.x * kMt;
-  if (UPPER && (n0 >> 6) < (m0 >> 6)) return;
-  const double* Ab = A + item * sA;
-  const double* Bb = B + item * sB;
-  double* Cb = Cm + item * sC;
+__device__ inline void dgemm_tile(const GemmArgs& g, int m0, int n0, int64_t item,
+                                  double (*red)[4][4][64]) {
+  if (UPPER && (n0 >> 6) < (m0 >> 6)) return;  // uniform over the workgroup
+  const double* Ab = g.A + item * g.sA;
+  const double* Bb = g.B + item * g.sB;
+  double* Cb = g.C + item * g.sC;
+  const int M = g.M, N = g.N, K = g.K;
+  const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int li = lane & 15, g = lane >> 4;
+  const int li = lane & 15, gq = lane >> 4;
   // this lane's A rows and opB columns; rows / columns past M / N read zeros
   const double* ap[2];
   const double* bp[2];
@@ -257,7 +267,7 @@ __global__ void __launch_bounds__(256)
     bp[h] = TRANSB ? Bb + static_cast<int64_t>(bok[h] ? n : 0) * ldb : Bb + (bok[h] ? n : 0);
   }
   auto load_chunk = [&](int kc, double (&a)[2][4], double (&b)[2][4]) {
-    const int kb = kc + 4 * g;
+    const int kb = kc + 4 * gq;
     const int cnt = K - kb < 0 ? 0 : (K - kb > 4 ? 4 : K - kb);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -296,7 +306,7 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
-  __shared__ double red[4][4][4][64];  // wave, block (2x+y), register, lane
+  // red[wave][block (2x+y)][register][lane]
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -311,12 +321,40 @@ __global__ void __launch_bounds__(256)
   for (int r = 0; r < 4; ++r) {
     const double v = ((red[0][wave][r][lane] + red[1][wave][r][lane]) + red[2][wave][r][lane]) +
                      red[3][wave][r][lane];
-    const int m = m0 + 16 * x + g + 4 * r;
+    const int m = m0 + 16 * x + gq + 4 * r;
     if (m < M && n < N) {
       double* p = Cb + static_cast<int64_t>(m) * ldc + n;
-      *p = beta == 0.0 ? alpha * v : alpha * v + beta * *p;
+      *p = g.beta == 0.0 ? g.alpha * v : g.alpha * v + g.beta * *p;
     }
   }
+}
+
+template <bool TRANSB, bool UPPER>
+__global__ void __launch_bounds__(256)
+    dgemm_kernel(GemmArgs g, const uint8_t* __restrict__ active,
+                 const uint8_t* __restrict__ failed) {
+  const int64_t item = blockIdx.z;
+  if (!active[item] || failed[item]) return;
+  __shared__ double red[4][4][4][64];
+  dgemm_tile<TRANSB, UPPER>(g, static_cast<int>(blockIdx.y) * kMt,
+                            static_cast<int>(blockIdx.x) * kMt, item, red);
+}
+
+// The two products of a recursion node that both follow P, in one launch:
+// A_TT -= P P^T (upper tiles; workgroups [0, tiles0)) and Q = P W_SS (the
+// rest). They read P and write disjoint memory.
+__global__ void __launch_bounds__(256)
+    dgemm_pair_kernel(GemmArgs g0, int nt0, int tiles0, GemmArgs g1, int nt1,
+                      const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
+  const int64_t item = blockIdx.z;
+  if (!active[item] || failed[item]) return;
+  __shared__ double red[4][4][4][64];
+  const int t = static_cast<int>(blockIdx.x);
+  if (t < tiles0)
+    dgemm_tile<true, true>(g0, (t / nt0) * kMt, (t % nt0) * kMt, item, red);
+  else
+    dgemm_tile<false, false>(g1, ((t - tiles0) / nt1) * kMt, ((t - tiles0) % nt1) * kMt, item,
+                             red);
 }
 
 // U = fp32(W) (upper), zero below the diagonal, for items that succeeded.
@@ -377,17 +415,30 @@ struct Ctx {
   hipStream_t s;
 };
 
+GemmArgs gemm_args(const double* A, int64_t lda, int64_t sA, const double* Bm, int64_t ldb,
+                   int64_t sB, double* Cm, int64_t ldc, int64_t sC, int64_t M, int64_t N,
+                   int64_t K, double alpha, double beta) {
+  return GemmArgs{A,  lda, sA, Bm, ldb, sB, Cm, ldc, sC, static_cast<int>(M), static_cast<int>(N),
+                  static_cast<int>(K), alpha, beta};
+}
+
 template <bool TRANSB, bool UPPER = false>
-int gemm(const Ctx& x, const double* A, int64_t lda, int64_t sA, const double* Bm, int64_t ldb,
-         int64_t sB, double* Cm, int64_t ldc, int64_t sC, int64_t M, int64_t N, int64_t K,
-         double alpha, double beta) {
-  dim3 grid(static_cast<unsigned>(ceil_div(N, kMt)), static_cast<unsigned>(ceil_div(M, kMt)),
+int gemm(const Ctx& x, const GemmArgs& g) {
+  dim3 grid(static_cast<unsigned>(ceil_div(g.N, kMt)), static_cast<unsigned>(ceil_div(g.M, kMt)),
             static_cast<unsigned>(x.B));
-  dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(A, lda, sA, Bm, ldb, sB, Cm, ldc, sC,
-                                                     static_cast<int>(M), static_cast<int>(N),
-                                                     static_cast<int>(K), alpha, beta, x.active,
-                                                     x.failed);
+  dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(g, x.active, x.failed);
   return check_launch("hinv gemm");
+}
+
+// g0 with TRANSB and UPPER, g1 plain, in one launch
+int gemm_pair(const Ctx& x, const GemmArgs& g0, const GemmArgs& g1) {
+  const int nt0 = static_cast<int>(ceil_div(g0.N, kMt));
+  const int tiles0 = nt0 * static_cast<int>(ceil_div(g0.M, kMt));
+  const int nt1 = static_cast<int>(ceil_div(g1.N, kMt));
+  const int tiles1 = nt1 * static_cast<int>(ceil_div(g1.M, kMt));
+  dim3 grid(static_cast<unsigned>(tiles0 + tiles1), 1, static_cast<unsigned>(x.B));
+  dgemm_pair_kernel<<<grid, 256, 0, x.s>>>(g0, nt0, tiles0, g1, nt1, x.active, x.failed);
+  return check_launch("hinv gemm pair");
 }
 
 int factor_rec(const Ctx& x, int64_t b0, int64_t b1, int depth) {
@@ -404,21 +455,21 @@ int factor_rec(const Ctx& x, int64_t b0, int64_t b1, int depth) {
   if (int rc = factor_rec(x, mid, b1, depth + 1)) return rc;
   const double* Wss = x.W + rm * C + rm;
   // P = A_TS W_SS^T
-  if (int rc = gemm<true>(x, x.A + r0 * C + rm, C, CC, Wss, C, CC, x.P, s2, h * s2, h, s2, s2,
-                          1.0, 0.0))
+  if (int rc = gemm<true>(x, gemm_args(x.A + r0 * C + rm, C, CC, Wss, C, CC, x.P, s2, h * s2, h,
+                                       s2, s2, 1.0, 0.0)))
     return rc;
-  // A_TT -= P P^T (upper tiles)
-  if (int rc = gemm<true, true>(x, x.P, s2, h * s2, x.P, s2, h * s2, x.A + r0 * C + r0, C, CC, h,
-                                h, s2, -1.0, 1.0))
-    return rc;
-  // Q = P W_SS
+  // A_TT -= P P^T (upper tiles) and Q = P W_SS
   double* Q = x.Q[depth];
-  if (int rc = gemm<false>(x, x.P, s2, h * s2, Wss, C, CC, Q, s2, h * s2, h, s2, s2, 1.0, 0.0))
+  if (int rc = gemm_pair(x,
+                         gemm_args(x.P, s2, h * s2, x.P, s2, h * s2, x.A + r0 * C + r0, C, CC, h,
+                                   h, s2, -1.0, 1.0),
+                         gemm_args(x.P, s2, h * s2, Wss, C, CC, Q, s2, h * s2, h, s2, s2, 1.0,
+                                   0.0)))
     return rc;
   if (int rc = factor_rec(x, b0, mid, depth + 1)) return rc;
   // W_TS = -W_TT Q
-  return gemm<false>(x, x.W + r0 * C + r0, C, CC, Q, s2, h * s2, x.W + r0 * C + rm, C, CC, h, s2,
-                     h, -1.0, 0.0);
+  return gemm<false>(x, gemm_args(x.W + r0 * C + r0, C, CC, Q, s2, h * s2, x.W + r0 * C + rm, C,
+                                  CC, h, s2, h, -1.0, 0.0));
 }
 
 }  // namespace
