@@ -357,6 +357,156 @@ __global__ void __launch_bounds__(256)
                              red);
 }
 
+// 64 x 64 output tiles for the large products (both edges >= kBigEdge): wave
+// (wr, wc) computes its 32 x 32 quadrant as 2 x 2 MFMA blocks over the whole
+// K, so there is no cross-wave reduction. Per 16-k chunk the workgroup stages
+// A rows and op(B) columns (as rows, [n][k]) in LDS with 16-byte loads, the
+// next chunk's loads in flight while the current one is multiplied (two LDS
+// buffers, one barrier per chunk; a 32-k chunk is 32 MFMAs per wave, enough
+// to cover the loads). Lane l of k-step (h, t) reads k = chunk + 16 h +
+// 4(l/16) + t for both operands (t = 0..3), one 32-byte LDS read per
+// operand row and h. The row stride of 34 doubles keeps eight consecutive
+// rows on distinct banks.
+constexpr int kBt = 64, kBk = 32, kBs = kBk + 2, kBigEdge = 768;
+
+struct Big64Lds {
+  double a[2][kBt][kBs];
+  double b[2][kBt][kBs];
+};
+
+template <bool TRANSB, bool UPPER>
+__device__ inline void dgemm64_tile(const GemmArgs& g, int m0, int n0, int64_t item,
+                                    Big64Lds& s) {
+  if (UPPER && (n0 >> 6) < (m0 >> 6)) return;  // uniform over the workgroup
+  const double* Ab = g.A + item * g.sA;
+  const double* Bb = g.B + item * g.sB;
+  double* Cb = g.C + item * g.sC;
+  const int M = g.M, N = g.N, K = g.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  const int li = lane & 15, gq = lane >> 4;
+  // staging: A rows (and op(B) rows when TRANSB) as thread t -> row t / 4,
+  // k 8 (t % 4) .. + 7; op(B) when B is [K][N]: k t / 8, columns 8 (t % 8) .. + 7
+  const int ar = tid >> 2, ak = 8 * (tid & 3);
+  const int bk = tid >> 3, bn = 8 * (tid & 7);
+  auto cnt4 = [](int left) { return left < 0 ? 0 : (left > 4 ? 4 : left); };
+  auto fetch = [&](int kc, double (&va)[8], double (&vb)[8]) {
+    const int m = m0 + ar;
+    const double* pa = Ab + static_cast<int64_t>(m < M ? m : 0) * g.lda + kc + ak;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      load4(pa + 4 * h, 1, m < M ? cnt4(K - kc - ak - 4 * h) : 0,
+            *reinterpret_cast<double(*)[4]>(&va[4 * h]));
+    if (TRANSB) {
+      const int n = n0 + ar;
+      const double* pb = Bb + static_cast<int64_t>(n < N ? n : 0) * g.ldb + kc + ak;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        load4(pb + 4 * h, 1, n < N ? cnt4(K - kc - ak - 4 * h) : 0,
+              *reinterpret_cast<double(*)[4]>(&vb[4 * h]));
+    } else {
+      const int k = kc + bk, n = n0 + bn;
+      const double* pb = Bb + static_cast<int64_t>(k < K ? k : 0) * g.ldb + n;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        load4(pb + 4 * h, 1, k < K ? cnt4(N - n - 4 * h) : 0,
+              *reinterpret_cast<double(*)[4]>(&vb[4 * h]));
+    }
+  };
+  auto stage = [&](int buf, const double (&va)[8], const double (&vb)[8]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f64x2_t*>(&s.a[buf][ar][ak + 2 * q]) = f64x2_t{va[2 * q], va[2 * q + 1]};
+    if (TRANSB) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f64x2_t*>(&s.b[buf][ar][ak + 2 * q]) = f64x2_t{vb[2 * q], vb[2 * q + 1]};
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s.b[buf][bn + t][bk] = vb[t];
+    }
+  };
+  f64x4_t acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+  const int nch = (K + kBk - 1) / kBk;
+  double va[8], vb[8];
+  fetch(0, va, vb);
+  stage(0, va, vb);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    const bool more = c + 1 < nch;
+    if (more) fetch((c + 1) * kBk, va, vb);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      double a[2][4], b[2][4];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const f64x2_t* pa =
+            reinterpret_cast<const f64x2_t*>(&s.a[buf][wr + 16 * x + li][16 * h + 4 * gq]);
+        const f64x2_t lo = pa[0], hi = pa[1];
+        a[x][0] = lo.x, a[x][1] = lo.y, a[x][2] = hi.x, a[x][3] = hi.y;
+        const f64x2_t* pb =
+            reinterpret_cast<const f64x2_t*>(&s.b[buf][wc + 16 * x + li][16 * h + 4 * gq]);
+        const f64x2_t blo = pb[0], bhi = pb[1];
+        b[x][0] = blo.x, b[x][1] = blo.y, b[x][2] = bhi.x, b[x][3] = bhi.y;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[x][t], b[y][t], acc[x][y], 0, 0, 0);
+    }
+    if (more) stage(buf ^ 1, va, vb);
+    __syncthreads();
+  }
+  // result register r of lane l of block (x, y) = D[l/16 + 4r][l%16]
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int n = n0 + wc + 16 * y + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wr + 16 * x + gq + 4 * r;
+        if (m < M && n < N) {
+          double* p = Cb + static_cast<int64_t>(m) * g.ldc + n;
+          *p = g.beta == 0.0 ? g.alpha * acc[x][y][r] : g.alpha * acc[x][y][r] + g.beta * *p;
+        }
+      }
+    }
+}
+
+template <bool TRANSB, bool UPPER>
+__global__ void __launch_bounds__(256)
+    dgemm64_kernel(GemmArgs g, const uint8_t* __restrict__ active,
+                   const uint8_t* __restrict__ failed) {
+  const int64_t item = blockIdx.z;
+  if (!active[item] || failed[item]) return;
+  __shared__ __attribute__((aligned(16))) Big64Lds s;
+  dgemm64_tile<TRANSB, UPPER>(g, static_cast<int>(blockIdx.y) * kBt,
+                              static_cast<int>(blockIdx.x) * kBt, item, s);
+}
+
+__global__ void __launch_bounds__(256)
+    dgemm64_pair_kernel(GemmArgs g0, int nt0, int tiles0, GemmArgs g1, int nt1,
+                        const uint8_t* __restrict__ active, const uint8_t* __restrict__ failed) {
+  const int64_t item = blockIdx.z;
+  if (!active[item] || failed[item]) return;
+  __shared__ __attribute__((aligned(16))) Big64Lds s;
+  const int t = static_cast<int>(blockIdx.x);
+  if (t < tiles0)
+    dgemm64_tile<true, true>(g0, (t / nt0) * kBt, (t % nt0) * kBt, item, s);
+  else
+    dgemm64_tile<false, false>(g1, ((t - tiles0) / nt1) * kBt, ((t - tiles0) % nt1) * kBt,
+                               item, s);
+}
+
 // U = fp32(W) (upper), zero below the diagonal, for items that succeeded.
 __global__ void emit_u_kernel(const double* __restrict__ W, int64_t C,
                               const uint8_t* __restrict__ active,
@@ -422,22 +572,35 @@ GemmArgs gemm_args(const double* A, int64_t lda, int64_t sA, const double* Bm, i
                   static_cast<int>(K), alpha, beta};
 }
 
+bool big(const GemmArgs& g) { return g.M >= kBigEdge && g.N >= kBigEdge; }
+
 template <bool TRANSB, bool UPPER = false>
 int gemm(const Ctx& x, const GemmArgs& g) {
-  dim3 grid(static_cast<unsigned>(ceil_div(g.N, kMt)), static_cast<unsigned>(ceil_div(g.M, kMt)),
-            static_cast<unsigned>(x.B));
-  dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(g, x.active, x.failed);
+  if (big(g)) {
+    dim3 grid(static_cast<unsigned>(ceil_div(g.N, kBt)), static_cast<unsigned>(ceil_div(g.M, kBt)),
+              static_cast<unsigned>(x.B));
+    dgemm64_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(g, x.active, x.failed);
+  } else {
+    dim3 grid(static_cast<unsigned>(ceil_div(g.N, kMt)), static_cast<unsigned>(ceil_div(g.M, kMt)),
+              static_cast<unsigned>(x.B));
+    dgemm_kernel<TRANSB, UPPER><<<grid, 256, 0, x.s>>>(g, x.active, x.failed);
+  }
   return check_launch("hinv gemm");
 }
 
 // g0 with TRANSB and UPPER, g1 plain, in one launch
 int gemm_pair(const Ctx& x, const GemmArgs& g0, const GemmArgs& g1) {
-  const int nt0 = static_cast<int>(ceil_div(g0.N, kMt));
-  const int tiles0 = nt0 * static_cast<int>(ceil_div(g0.M, kMt));
-  const int nt1 = static_cast<int>(ceil_div(g1.N, kMt));
-  const int tiles1 = nt1 * static_cast<int>(ceil_div(g1.M, kMt));
+  const bool b64 = big(g0) && big(g1);
+  const int64_t t = b64 ? kBt : kMt;
+  const int nt0 = static_cast<int>(ceil_div(g0.N, t));
+  const int tiles0 = nt0 * static_cast<int>(ceil_div(g0.M, t));
+  const int nt1 = static_cast<int>(ceil_div(g1.N, t));
+  const int tiles1 = nt1 * static_cast<int>(ceil_div(g1.M, t));
   dim3 grid(static_cast<unsigned>(tiles0 + tiles1), 1, static_cast<unsigned>(x.B));
-  dgemm_pair_kernel<<<grid, 256, 0, x.s>>>(g0, nt0, tiles0, g1, nt1, x.active, x.failed);
+  if (b64)
+    dgemm64_pair_kernel<<<grid, 256, 0, x.s>>>(g0, nt0, tiles0, g1, nt1, x.active, x.failed);
+  else
+    dgemm_pair_kernel<<<grid, 256, 0, x.s>>>(g0, nt0, tiles0, g1, nt1, x.active, x.failed);
   return check_launch("hinv gemm pair");
 }
 

@@ -494,58 +494,96 @@ __global__ void __launch_bounds__(kWaves * 64)
 // W[row, i2 + m] -= sum_k Err[row, k] * U[b, i1 + k, i2 + m] (the reference's
 // deferred bmm): 64x64 output tiles, each wave a 32x32 block on
 // v_mfma_f32_32x32x2f32 (A[l%32][k], B[k][l%32] with k = l/32 per step; result
-// register r of lane l = D[8(r/4) + 4(l/32) + r%4][l%32]). Each lane loads
-// four consecutive k of its Err row with one 16-byte load and the matching
-// four U rows; step t of a chunk of 8 takes k = chunk + 4(l/32) + t for both
-// operands (the same permutation of k).
-constexpr int kTm = 64, kTn = 64;
+// register r of lane l = D[8(r/4) + 4(l/32) + r%4][l%32]). K goes in chunks of
+// 64: the workgroup stages the chunk's Err rows and U columns (transposed) in
+// LDS with 16-byte coalesced loads, then each lane reads four consecutive k
+// of its Err row and of its U column with one 16-byte LDS read each; step t
+// of an 8-k group takes k = group + 4(l/32) + t for both operands (the same
+// permutation of k in every build of this kernel, so the sums round the same
+// way). The tile's W values are loaded before the products and updated after
+// them.
+constexpr int kTm = 64, kTn = 64, kLzK = 64, kLzS = kLzK + 4;  // LDS row stride (floats)
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 __global__ void __launch_bounds__(256)
     lazy_update_kernel(float* __restrict__ W, const float* __restrict__ U,
                        const float* __restrict__ Err, int64_t B, int64_t R, int64_t C, int64_t i1,
                        int n) {
+  __shared__ __attribute__((aligned(16))) float sE[kTm][kLzS];  // Err[r0 + i][kc + k]
+  __shared__ __attribute__((aligned(16))) float sU[kTn][kLzS];  // U[i1 + kc + k][m0 + j], as [j][k]
   const int64_t i2 = i1 + n;
   const int64_t b = blockIdx.z;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTm + (wave >> 1) * 32;
-  const int64_t m0 = i2 + static_cast<int64_t>(blockIdx.x) * kTn + (wave & 1) * 32;
-  if (r0 >= R || m0 >= C) return;  // whole wave
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t R0 = static_cast<int64_t>(blockIdx.y) * kTm;
+  const int64_t M0 = i2 + static_cast<int64_t>(blockIdx.x) * kTn;
+  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
   const int li = lane & 31, g = lane >> 5;
-  const int64_t r = r0 + li, m = m0 + li;
-  const bool rok = r < R, mok = m < C;
-  const float* Ea = Err + (b * R + (rok ? r : 0)) * n;
-  const float* Ubk = U + b * C * C + i1 * C + (mok ? m : i2);
-  const bool vec = (n & 3) == 0;
+  const int64_t m = M0 + wc + li;
+  const bool mok = m < C;
+  // this lane's 16 outputs: rows R0 + wr + 8(i/4) + 4g + i%4, column m
+  float wv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t rr = R0 + wr + 8 * (i >> 2) + 4 * g + (i & 3);
+    wv[i] = (rr < R && mok) ? W[(b * R + rr) * C + m] : 0.0f;
+  }
+  const float* Eb = Err + b * R * n;
+  const float* Ub = U + b * C * C;
+  const bool vec = (n & 3) == 0 && (C & 3) == 0 && (i2 & 3) == 0;
   f32x16_t acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  for (int kc = 0; kc < n; kc += 8) {
-    const int kb = kc + 4 * g;
-    float a[4], u[4];
-    if (vec && kb + 4 <= n) {
-      const float4 v = *reinterpret_cast<const float4*>(Ea + kb);
-      a[0] = v.x, a[1] = v.y, a[2] = v.z, a[3] = v.w;
-    } else {
+  for (int kc = 0; kc < n; kc += kLzK) {
+    // stage: thread t copies 16-byte pieces (row t / 16 + 16 p, k or column 4 (t % 16))
 #pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = kb + t < n ? Ea[kb + t] : 0.0f;
+    for (int p = 0; p < 4; ++p) {
+      const int rr = tid / 16 + 16 * p, c4 = 4 * (tid % 16);
+      // Err rows
+      {
+        const int64_t row = R0 + rr;
+        const int k = kc + c4;
+        float v[4];
+        if (vec && row < R && k + 4 <= n) {
+          const float4 q = *reinterpret_cast<const float4*>(Eb + row * n + k);
+          v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = (row < R && k + t < n) ? Eb[row * n + k + t] : 0.0f;
+        }
+        *reinterpret_cast<float4*>(&sE[rr][c4]) = float4{v[0], v[1], v[2], v[3]};
+      }
+      // U row i1 + kc + rr, columns M0 + c4 .. + 3, stored transposed
+      {
+        const int k = kc + rr;
+        const int64_t col = M0 + c4;
+        float v[4];
+        if (vec && k < n && col + 4 <= C) {
+          const float4 q = *reinterpret_cast<const float4*>(Ub + (i1 + k) * C + col);
+          v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = (k < n && col + t < C) ? Ub[(i1 + k) * C + col + t] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sU[c4 + t][rr] = v[t];
+      }
     }
+    __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 4; ++t) u[t] = kb + t < n ? Ubk[static_cast<int64_t>(kb + t) * C] : 0.0f;
-    if (!rok) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) a[t] = 0.0f;
+    for (int k8 = 0; k8 < kLzK; k8 += 8) {
+      const float4 a = *reinterpret_cast<const float4*>(&sE[wr + li][k8 + 4 * g]);
+      const float4 u = *reinterpret_cast<const float4*>(&sU[wc + li][k8 + 4 * g]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, u.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, u.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, u.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, u.w, acc, 0, 0, 0);
     }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t], u[t], acc, 0, 0, 0);
+    __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t rr = r0 + 8 * (i >> 2) + 4 * g + (i & 3);
-    if (rr < R && mok) {
-      float* p = W + (b * R + rr) * C + m;
-      *p = *p - acc[i];
-    }
+    const int64_t rr = R0 + wr + 8 * (i >> 2) + 4 * g + (i & 3);
+    if (rr < R && mok) W[(b * R + rr) * C + m] = wv[i] - acc[i];
   }
 }
 
