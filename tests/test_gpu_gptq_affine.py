@@ -106,6 +106,29 @@ def test_affine_matches_oracle(bits, G, clip, storage, block):
     _check_vs(W, q, s, b, W_dq, rq, rs, rb, rW, Hr)
 
 
+@pytest.mark.parametrize("case,w_mult,h_mult", [
+    ("tiny_H", 1.0, 1e-20),    # U's diagonal above 2^24: no RN(1/d), every error division exact-path
+    ("tiny_W", 1e-31, 1.0),    # numerators below 2^-100: the error divisions leave the fast range
+    ("huge_W", 1e31, 1.0),     # numerators above 2^101
+])
+def test_affine_out_of_range_operands_vs_oracle(case, w_mult, h_mult):
+    """The column loop divides with Markstein's correction and only records
+    operands outside its exact range; a group that met any is solved again
+    with the guarded division. These inputs put (almost) every group on that
+    second path; the codes, params and W_dq must still be the oracle's."""
+    from mlx_gptq import gptq
+
+    W, H, _ = _setup(B=2, R=64, C=256, N=1024, seed=11, scale=0.02, outliers=2)
+    W = W * w_mult
+    H = H * h_mult
+    Wg, Hg = W.clone().to(DEV), H.clone().to(DEV)
+    q, s, b, W_dq, _ = gptq.gptq_quantize(Wg, Hg, 4, 64, storage_dtype=torch.float32)
+    Wr, Hr = W.clone(), H.clone()
+    rq, rs, rb, rW, _ = gptq_ref.gptq_quantize(Wr, Hr, 4, 64, storage_dtype=torch.float32)
+    assert torch.isfinite(W_dq).all()
+    _check_vs(W, q, s, b, W_dq, rq, rs, rb, rW, Hr)
+
+
 def test_affine_config1_shape_vs_oracle():
     """BASELINE config 1 (single Linear 2048x2048, affine 4-bit, G=64, block
     128, MSE clip) at its real size, on 8192 lognormal tokens with 1% x20
