@@ -92,6 +92,18 @@ def _counter(name: str, kernel_prefix: str, key: str):
     return max(hits) if hits else None
 
 
+def _counters_in_order(name: str, kernel_prefix: str, key: str):
+    """The same figure for every distinct dispatch of a kernel, in launch
+    order (profiles/<name>_counters.json keeps the first dispatch of each
+    grid size, in the order the profiled step launched them)."""
+    p = os.path.join(ROOT, "profiles", f"{name}_counters.json")
+    if not os.path.exists(p):
+        return []
+    with open(p) as f:
+        per = json.load(f).get("per_dispatch", {})
+    return [v[key] for k, v in per.items() if k.startswith(kernel_prefix) and key in v]
+
+
 def _roofline(kernel, bound, amount, ms, traffic=None):
     """amount: flops (bound "mfma": bf16 MFMA peak; "fp64": fp64 peak) or bytes
     (bound "hbm") per launch."""
@@ -578,8 +590,17 @@ def run_dense(args, torch, np) -> int:
     config = {"workload": L.name, "elements": elements,
               "matrices": {m.name: list(m.W.shape[1:]) for m in L.mats},
               "tokens": {k: int(X.shape[0]) for k, X in L.inputs.items()}}
-    _line(args, value, ms_step, config, phases, rooflines[dom], cpu, setup_s,
-          {"phase_rooflines": rooflines})
+    extra = {"phase_rooflines": rooflines}
+    # rocprofv3 counters of this config's committed profile (one SYRK
+    # dispatch per calibration input, in the step's launch order)
+    utils = _counters_in_order(tag, "mgq::syrk_kernel<false", "mfma_util_pct")
+    if len(utils) == len(keys):
+        extra["hessian_mfma_util_pct"] = dict(zip(keys, utils))
+    busy = _counters_in_order(tag, "mgq::mxfp_solve_kernel", "valu_busy_pct")
+    busy += _counters_in_order(tag, "mgq::affine_block_kernel", "valu_busy_pct")
+    if busy:
+        extra["solve_valu_busy_pct"] = max(busy)
+    _line(args, value, ms_step, config, phases, rooflines[dom], cpu, setup_s, extra)
     return 0
 
 
