@@ -17,7 +17,7 @@ import logging
 import pytest
 import torch
 
-from oracle import gptq_ref
+from oracle import gptq_ref, hessian_ref
 from tests import golden_io
 
 pytestmark = pytest.mark.gpu
@@ -144,6 +144,28 @@ def test_affine_config1_shape_vs_oracle():
     q, s, b, W_dq, rel = gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), 4, 64)
     rq, rs, rb, rW, rrel = gptq_ref.solve_gptq(W, H.clone(), 4, 64)
     _check_vs(W.float(), q, s, b, W_dq, rq, rs, rb, rW, H)
+    assert torch.allclose(rel.cpu(), rrel, rtol=1e-2)
+
+
+def test_affine_config1_chain_full_size():
+    """Config 1 end to end as the bench runs it: the bf16 calibration rows in
+    a capture.Stash, H from Stash.hessian (the GPU SYRK), the affine solve on
+    the device; against the oracle's stash Hessian of the same rows (fp32
+    addmm, capture.py:68-76) and the oracle's solve."""
+    from mlx_gptq import capture, gptq, synth
+
+    L = synth.dense_config(1, device=DEV)
+    X, W = L.inputs["x"], L.mats[0].W
+    C = X.shape[1]
+    st = capture.Stash("x", C)
+    st.add(X)
+    H = st.hessian(torch.device(DEV)).unsqueeze(0)
+    Xc = X.cpu()
+    assert hessian_ref.rel_frobenius(H[0].cpu(), hessian_ref.hessian_fp64(Xc)) < 1e-5
+    q, s, b, W_dq, rel = gptq.solve_gptq(W, H.clone(), **L.mats[0].solve)
+    Hr = hessian_ref.stash_hessian([Xc], C).unsqueeze(0)
+    rq, rs, rb, rW, rrel = gptq_ref.solve_gptq(W.cpu(), Hr.clone(), 4, 64)
+    _check_vs(W.float().cpu(), q, s, b, W_dq, rq, rs, rb, rW, Hr)
     assert torch.allclose(rel.cpu(), rrel, rtol=1e-2)
 
 
