@@ -26,6 +26,7 @@ from __future__ import annotations
 import ctypes
 import logging
 import threading
+from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -67,6 +68,53 @@ def _as_offsets(offsets) -> np.ndarray:
     if np.any(np.diff(off) < 0) or off[0] < 0:
         raise ValueError("offsets must be non-negative and non-decreasing")
     return off
+
+
+# Plans and device workspaces of recent grouped Hessian launches, keyed by
+# (device, stream, C, offsets, target_items). A repeated launch (the same
+# stash shape, layer after layer) skips the host planning, the pinned plan
+# buffer, the workspace allocation and the plan's copy to the device. Launches
+# on one stream run in order, so a cached workspace never serves two launches
+# at once; other streams get their own entries.
+_WS_CACHE: "OrderedDict[tuple, tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
+_WS_CACHE_MAX_ENTRIES = 8
+_WS_CACHE_MAX_BYTES = 512 << 20
+_ws_lock = threading.Lock()
+
+
+def _hessian_plan(dev: torch.device, stream: int, C: int, off: np.ndarray, target_items: int):
+    """(plan, workspace): the pinned host plan and a device workspace that
+    starts with a copy of it."""
+    key = (dev.index, int(stream), C, off.tobytes(), int(target_items))
+    with _ws_lock:
+        hit = _WS_CACHE.get(key)
+        if hit is not None:
+            _WS_CACHE.move_to_end(key)
+            return hit
+    lib = nat.load()
+    G = off.size - 1
+    plan_bytes = ctypes.c_int64(0)
+    ws_bytes = ctypes.c_int64(0)
+    nat.check(
+        lib.mgq_hessian_plan(C, G, off.ctypes.data, int(target_items), None, 0,
+                             ctypes.byref(plan_bytes), ctypes.byref(ws_bytes)),
+        "mgq_hessian_plan",
+    )
+    plan = torch.empty(plan_bytes.value, dtype=torch.uint8, pin_memory=True)
+    nat.check(
+        lib.mgq_hessian_plan(C, G, off.ctypes.data, int(target_items), plan.data_ptr(),
+                             plan_bytes.value, None, None),
+        "mgq_hessian_plan",
+    )
+    ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=dev)
+    ws[: plan_bytes.value].copy_(plan, non_blocking=True)
+    with _ws_lock:
+        _WS_CACHE[key] = (plan, ws)
+        total = sum(w.numel() for _, w in _WS_CACHE.values())
+        while _WS_CACHE and (len(_WS_CACHE) > _WS_CACHE_MAX_ENTRIES or total > _WS_CACHE_MAX_BYTES):
+            _, (_, w) = _WS_CACHE.popitem(last=False)
+            total -= w.numel()
+    return plan, ws
 
 
 def grouped_hessian(
@@ -111,26 +159,12 @@ def grouped_hessian(
         accumulate = False
     elif out.shape != (G, C, C) or out.dtype != torch.float32 or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous float32 [{G}, {C}, {C}] tensor")
-    lib = nat.load()
-    plan_bytes = ctypes.c_int64(0)
-    ws_bytes = ctypes.c_int64(0)
-    nat.check(
-        lib.mgq_hessian_plan(C, G, off.ctypes.data, int(target_items), None, 0,
-                             ctypes.byref(plan_bytes), ctypes.byref(ws_bytes)),
-        "mgq_hessian_plan",
-    )
-    plan = torch.empty(plan_bytes.value, dtype=torch.uint8, pin_memory=True)
-    nat.check(
-        lib.mgq_hessian_plan(C, G, off.ctypes.data, int(target_items), plan.data_ptr(),
-                             plan_bytes.value, None, None),
-        "mgq_hessian_plan",
-    )
-    ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=dev)
-    ws[: plan_bytes.value].copy_(plan, non_blocking=True)
+    stream = nat.stream_of(dev)
+    plan, ws = _hessian_plan(dev, stream, C, off, target_items)
     nat.call(
         "mgq_hessian", X.data_ptr(), int(X.shape[0]), X.stride(0), C,
         None if row_index is None else row_index.data_ptr(), plan.data_ptr(), out.data_ptr(),
-        1 if accumulate else 0, ws.data_ptr(), ws_bytes.value, nat.stream_of(dev),
+        1 if accumulate else 0, ws.data_ptr(), ws.numel(), stream,
     )
     return out
 
