@@ -94,9 +94,12 @@ __global__ void build_kernel(const float* __restrict__ H, int64_t C, const float
 // from the two published rows itself, with the same operations the lanes
 // holding row j - 1 apply to it (so the result is bitwise that of single
 // steps). Each lane reads the entries of its 8 rows, its 2 columns and the
-// pivots of both rows: 32 FMAs of update per lane and pair. Only the lower
-// triangle of the block is read; rows past n are identity padding. A pivot
-// <= 0 or NaN flags the item as failed.
+// pivots of both rows: 32 FMAs of update per lane and pair. The sweep is
+// bound by instruction issue (one wave per SIMD), so the rows a step updates
+// are selected by exec masks over two lane sets rather than by per-row
+// selects, and rows at or past the pivot are not touched at all. Only the
+// lower triangle of the block is read; rows past n are identity padding. A
+// pivot <= 0 or NaN flags the item as failed.
 __global__ void __launch_bounds__(256)
     leaf_kernel(const double* __restrict__ A, double* __restrict__ W, int64_t C, int64_t r0, int n,
                 const uint8_t* __restrict__ active, uint8_t* __restrict__ failed) {
@@ -155,15 +158,35 @@ __global__ void __launch_bounds__(256)
       piv[jr] = own_row ? d : piv[jr];
       piv[jr - 1] = own_row ? d1 : piv[jr - 1];
       const bool col_j = (k0 == j - 1);  // this lane holds columns j - 1 and j
-      // step j
+      // Row i = 8p + r takes step j when i < j: every row of a lane with
+      // p < jp, the rows r < jr of the lanes with p == jp. The two lane sets
+      // run as exec-masked blocks, so rows past the pivot are not touched
+      // and no per-row select is needed; only the wave holding column j
+      // enters the block that writes X[i][j] = -c_i.
+      double cf[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const bool upd = 8 * p + r < j;
-        const double cf = upd ? ai[r] * rd : 0.0;
-        R[r][0] = fma(-cf, ak.x, R[r][0]);
-        R[r][1] = fma(-cf, ak.y, R[r][1]);
-        // column j of the inverse: X[i][j] = -c_i
-        R[r][1] = (upd && col_j) ? -cf : R[r][1];
+      for (int r = 0; r < 8; ++r) cf[r] = ai[r] * rd;
+      if (p <= jp) {
+#pragma unroll
+        for (int r = 0; r < jr; ++r) {
+          R[r][0] = fma(-cf[r], ak.x, R[r][0]);
+          R[r][1] = fma(-cf[r], ak.y, R[r][1]);
+        }
+        if (col_j) {
+#pragma unroll
+          for (int r = 0; r < jr; ++r) R[r][1] = -cf[r];
+        }
+      }
+      if (p < jp) {
+#pragma unroll
+        for (int r = jr; r < 8; ++r) {
+          R[r][0] = fma(-cf[r], ak.x, R[r][0]);
+          R[r][1] = fma(-cf[r], ak.y, R[r][1]);
+        }
+        if (col_j) {
+#pragma unroll
+          for (int r = jr; r < 8; ++r) R[r][1] = -cf[r];
+        }
       }
       // row j - 1 after step j, at this lane's rows and columns
       double a1[8];
@@ -171,14 +194,30 @@ __global__ void __launch_bounds__(256)
       for (int r = 0; r < 8; ++r) a1[r] = fma(-cj, ai[r], bi[r]);
       const double ak1x = fma(-cj, ak.x, bk.x);
       const double ak1y = col_j ? -cj : fma(-cj, ak.y, bk.y);
-      // step j - 1
+      // step j - 1: rows i < j - 1
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const bool upd = 8 * p + r < j - 1;
-        const double cf = upd ? a1[r] * rd1 : 0.0;
-        R[r][0] = fma(-cf, ak1x, R[r][0]);
-        R[r][1] = fma(-cf, ak1y, R[r][1]);
-        R[r][0] = (upd && col_j) ? -cf : R[r][0];
+      for (int r = 0; r < 8; ++r) cf[r] = a1[r] * rd1;
+      if (p <= jp) {
+#pragma unroll
+        for (int r = 0; r < jr - 1; ++r) {
+          R[r][0] = fma(-cf[r], ak1x, R[r][0]);
+          R[r][1] = fma(-cf[r], ak1y, R[r][1]);
+        }
+        if (col_j) {
+#pragma unroll
+          for (int r = 0; r < jr - 1; ++r) R[r][0] = -cf[r];
+        }
+      }
+      if (p < jp) {
+#pragma unroll
+        for (int r = jr - 1; r < 8; ++r) {
+          R[r][0] = fma(-cf[r], ak1x, R[r][0]);
+          R[r][1] = fma(-cf[r], ak1y, R[r][1]);
+        }
+        if (col_j) {
+#pragma unroll
+          for (int r = jr - 1; r < 8; ++r) R[r][0] = -cf[r];
+        }
       }
     }
   }
