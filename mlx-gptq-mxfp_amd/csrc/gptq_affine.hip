@@ -224,10 +224,12 @@ __global__ void __launch_bounds__(kWaves * 64)
                         int64_t C, int64_t i1, int n, int G, float maxq, int storage, Shrinks sh,
                         uint8_t* __restrict__ q_out, void* s_store, void* b_store,
                         float* __restrict__ Err) {
-  extern __shared__ float smem[];  // errs [kWaves][n], then (LDSU) Ublk [n][n]
+  // column table [kWaves][G] (float4), errs [kWaves][n], then (LDSU) Ublk [n][n]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* errs = smem + wave * n;
-  float* Ublk = smem + kWaves * n;
+  float4* ctab = reinterpret_cast<float4*>(smem) + wave * G;
+  float* errs = smem + kWaves * 4 * G + wave * n;
+  float* Ublk = smem + kWaves * 4 * G + kWaves * n;
   const int64_t b = blockIdx.y;
   const float* Ub = U + b * C * C;
   if constexpr (LDSU) {
@@ -260,6 +262,8 @@ __global__ void __launch_bounds__(kWaves * 64)
   }
   const int64_t r_in = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
   if (r_in >= R) return;  // whole wave exits together (no block barriers below)
+  // canonicalized once, so that the clamps in affine_round do not redo it
+  maxq = __builtin_canonicalizef(maxq);
   const int64_t row = b * R + r_in;
   float* Wr = W + row * C;
   const int64_t ng = C / G;
@@ -399,74 +403,112 @@ __global__ void __launch_bounds__(kWaves * 64)
     float acc0[CPL];
 #pragma unroll
     for (int s = 0; s < CPL; ++s) acc0[s] = acc[s];
+    // A divisor whose reciprocal is 0 (outside [2^-24, 2^24]) sends the
+    // group to the guarded division directly.
+    bool y_zero = !(ysafe != 0.0f);
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) y_zero |= act[s] & !(yd[s] != 0.0f);
+    y_zero = __builtin_amdgcn_ballot_w64(y_zero) != 0;
+    // the column table: U[c][c], RN(1 / U[c][c]) and U[c][c+1] for column
+    // c, read by the whole wave with one LDS read per column
+#pragma unroll
+    for (int s = 0; s < CPL; ++s) {
+      const int col = lane + 64 * s;
+      if (act[s]) {
+        const int cn = col + 1 < G ? col + 1 : col;
+        const float u1 = col + 1 < G ? (LDSU ? Ublk[(j - i1 + col) * n + (j - i1 + cn)]
+                                             : Ub[(j + col) * C + j + cn])
+                                     : 0.0f;
+        ctab[col] = float4{dg[s], yd[s], u1, 0.0f};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     auto run_columns = [&](auto exact_tag) __attribute__((always_inline)) {
       constexpr bool EXACT = decltype(exact_tag)::value;
-      bool slow = false;
+      // The numerators' smallest nonzero magnitude (as its bit pattern
+      // shifted left by one, minus 2, so that a zero wraps to the top) and
+      // their largest magnitude. The correction is exact when every nonzero
+      // numerator has a biased exponent in [27, 227] (div_slow).
+      uint32_t mag_lo = 0xffffffffu;
+      float mag_hi = 0.0f;
       float wn = lane_read(acc[0], 0);
-      auto column = [&](int c, const float (&uc)[CPL]) __attribute__((always_inline)) {
-        const int owner = c & 63, slot = c >> 6;
-        const int c1 = c + 1 < G ? c + 1 : c;
+      // column c; c1 = c + 1 (c for the last column)
+      auto column = [&](int c, int c1, const float (&uc)[CPL]) __attribute__((always_inline)) {
         const int owner1 = c1 & 63, slot1 = c1 >> 6;
-        float diag_v = dg[0], yd_v = yd[0], pre_v = acc[0], u_v = uc[0];
+        float pre_v = acc[0];
 #pragma unroll
-        for (int s = 1; s < CPL; ++s) {
-          if (s == slot) {
-            diag_v = dg[s];
-            yd_v = yd[s];
-          }
-          if (s == slot1) {
-            pre_v = acc[s];
-            u_v = uc[s];
-          }
-        }
-        const float diag = lane_read(diag_v, owner), ydg = lane_read(yd_v, owner);
-        const float pre1 = lane_read(pre_v, owner1), u1 = lane_read(u_v, owner1);
+        for (int s = 1; s < CPL; ++s)
+          if (s == slot1) pre_v = acc[s];
+        const float4 ct = ctab[c];
+        const float diag = ct.x, ydg = ct.y, u1 = ct.z;
+        const float pre1 = lane_read(pre_v, owner1);
         float e;
         if constexpr (EXACT) {
           const float q = affine_q(wn, b32, s_safe, ysafe, maxq);
           const float dq = q * s32 + b32;
           e = div_pos(wn - dq, diag, ydg);
         } else {
+          // a zero numerator's quotient is that zero: copysign turns the
+          // correction's +0 into it (every other quotient has its sign)
           const float n1 = wn - b32;
-          const float t1 = div_fast(n1, s_safe, ysafe);
-          const float q = affine_round(n1 == 0.0f ? n1 : t1, maxq);
+          const float q = affine_round(copysignf(div_fast(n1, s_safe, ysafe), n1), maxq);
           const float dq = q * s32 + b32;
           const float n2 = wn - dq;
-          const float t2 = div_fast(n2, diag, ydg);
-          e = n2 == 0.0f ? n2 : t2;
-          slow |= div_slow(n1, ysafe) | div_slow(n2, ydg);
+          e = copysignf(div_fast(n2, diag, ydg), n2);
+          mag_lo = min(mag_lo, min((f2u(n1) << 1) - 2u, (f2u(n2) << 1) - 2u));
+          mag_hi = fmaxf(mag_hi, fmaxf(fabsf(n1), fabsf(n2)));
         }
 #pragma unroll
         for (int s = 0; s < CPL; ++s) acc[s] = lane + 64 * s > c ? acc[s] - e * uc[s] : acc[s];
         wn = pre1 - e * u1;
       };
-      // U rows arrive eight columns ahead (rows past the group repeat its last)
+      // Row c of the group's U block at urow + c * ust. Rows arrive eight
+      // columns ahead; the last eight full columns load nothing, and the
+      // columns past the last multiple of 8 load their own rows.
+      const float* urow = LDSU ? Ublk + (j - i1) * n + (j - i1) : Ub + j * C + j;
+      const int64_t ust = LDSU ? n : C;
+      // (lanes past the group read the row's first entry: their values are
+      // never read)
+      auto load_row = [&](const float* p, float (&u)[CPL]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < CPL; ++s) u[s] = p[act[s] ? lane + 64 * s : 0];
+      };
       const int G8 = G & ~7;
       float ring[8][CPL];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + (u < G ? u : G - 1), j, lane, act, ring[u]);
-      for (int c0 = 0; c0 < G8; c0 += 8) {
+      for (int u = 0; u < 8; ++u) load_row(urow + (u < G ? u : G - 1) * ust, ring[u]);
+      const float* unext = urow + 8 * ust;
+      int c0 = 0;
+      for (; c0 + 8 < G8; c0 += 8) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const int c = c0 + u;
           float uc[CPL];
 #pragma unroll
           for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
-          const int nxt = c + 8 < G ? c + 8 : G - 1;
-          load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + nxt, j, lane, act, ring[u]);
-          column(c, uc);
+          load_row(unext, ring[u]);
+          unext += ust;
+          column(c0 + u, c0 + u + 1, uc);
+        }
+      }
+      if (G8 > 0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int c = c0 + u;
+          column(c, c + 1 < G ? c + 1 : c, ring[u]);
         }
       }
       for (int c = G8; c < G; ++c) {
         float uc[CPL];
-        load_urow<CPL, LDSU>(Ub, Ublk, C, i1, n, j + c, j, lane, act, uc);
-        column(c, uc);
+        load_row(urow + c * ust, uc);
+        column(c, c + 1 < G ? c + 1 : c, uc);
       }
-      return slow;
+      // nonzero numerators below 2^-100, or any at or above 2^101 (NaN
+      // quotients are NaN either way)
+      return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f);
     };
-    // every lane computed the same chain, so `slow` is wave-uniform
-    if (__builtin_amdgcn_ballot_w64(run_columns(std::false_type{})) != 0) {
+    // every lane computed the same chain, so its verdict is wave-uniform
+    if (y_zero || __builtin_amdgcn_ballot_w64(run_columns(std::false_type{})) != 0) {
 #pragma unroll
       for (int s = 0; s < CPL; ++s) acc[s] = acc0[s];
       run_columns(std::true_type{});
@@ -657,7 +699,8 @@ extern "C" int mgq_gptq_affine_block(float* W, const float* U, int64_t B, int64_
   const dim3 blocks(static_cast<unsigned>(ceil_div(R, kWaves)), static_cast<unsigned>(B));
   const float maxq = static_cast<float>((1 << bits) - 1);
   const bool ldsu = n <= kLdsBlock;
-  const size_t lds = sizeof(float) * (kWaves * static_cast<size_t>(n) +
+  const size_t lds = sizeof(float) * (kWaves * 4 * static_cast<size_t>(group_size) +
+                                      kWaves * static_cast<size_t>(n) +
                                       (ldsu ? static_cast<size_t>(n) * n : 0));
 #define AFFINE_LAUNCH(CPL_, LDSU_)                                                          \
   affine_block_kernel<CPL_, LDSU_><<<blocks, kWaves * 64, lds, s>>>(                        \
