@@ -62,31 +62,39 @@ __device__ inline float2 swap16(float v) {
   return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
-// N sums in one butterfly: v[i] <- v[i] + partner at every step, the
-// rounding of an xor butterfly with __shfl_xor. Because a + b == b + a,
-// both lanes of a pair hold the same bits after each step: the xor-32/16
-// sums are lo + hi in every lane, and after the 8 step a lane's value
-// depends only on lane mod 8, so a rotation by 4 reads the value of lane ^ 4.
+// N wave sums (N a multiple of 4), each rounded like an xor butterfly with
+// __shfl_xor (v <- v + partner for xor 32, 16, 8, 4, 2, 1), by recursive
+// halving. The xor-32 step swaps v[i] with v[i + N/2], so lanes 0-31 keep
+// sum i and lanes 32-63 sum i + N/2, both as lo + hi; the xor-16 step pairs
+// those results the same way (row 2k + row 2k+1); the DPP steps then run on
+// N/4 values. Because a + b == b + a bit for bit, after the 8 step a lane's
+// value depends only on lane mod 8, so a rotation by 4 reads the value of
+// lane ^ 4. Sum i + (N/4) r ends in u[i] of the lanes of row r (lanes 16r ..
+// 16r + 15).
 template <int N>
-__device__ inline void wave_sum_n(float (&v)[N]) {
+__device__ inline void wave_sum_halving(const float (&v)[N], float (&u)[N / 4]) {
+  static_assert(N % 4 == 0, "N must be a multiple of 4");
+  float w[N / 2];
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const float2 s = swap32(v[i]);
-    v[i] = s.x + s.y;
+  for (int i = 0; i < N / 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
+                                                    __float_as_uint(v[i + N / 2]), false, false);
+    w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const float2 s = swap16(v[i]);
-    v[i] = s.x + s.y;
+  for (int i = 0; i < N / 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[i]),
+                                                    __float_as_uint(w[i + N / 4]), false, false);
+    u[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppRor8>(v[i]);
+  for (int i = 0; i < N / 4; ++i) u[i] += dpp_read<kDppRor8>(u[i]);
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppRor4>(v[i]);
+  for (int i = 0; i < N / 4; ++i) u[i] += dpp_read<kDppRor4>(u[i]);
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppXor2>(v[i]);
+  for (int i = 0; i < N / 4; ++i) u[i] += dpp_read<kDppXor2>(u[i]);
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_read<kDppXor1>(v[i]);
+  for (int i = 0; i < N / 4; ++i) u[i] += dpp_read<kDppXor1>(u[i]);
 }
 
 // wave_nan_min and wave_nan_max of two values in one xor butterfly, each
@@ -224,12 +232,14 @@ __global__ void __launch_bounds__(kWaves * 64)
                         int64_t C, int64_t i1, int n, int G, float maxq, int storage, Shrinks sh,
                         uint8_t* __restrict__ q_out, void* s_store, void* b_store,
                         float* __restrict__ Err) {
-  // column table [kWaves][G] (float4), errs [kWaves][n], then (LDSU) Ublk [n][n]
+  // per-wave table [kWaves][max(G, 64)] (float4: the clip candidates, then
+  // the column table), errs [kWaves][n], then (LDSU) Ublk [n][n]
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float4* ctab = reinterpret_cast<float4*>(smem) + wave * G;
-  float* errs = smem + kWaves * 4 * G + wave * n;
-  float* Ublk = smem + kWaves * 4 * G + kWaves * n;
+  const int tab_n = G > 64 ? G : 64;
+  float4* ctab = reinterpret_cast<float4*>(smem) + wave * tab_n;
+  float* errs = smem + kWaves * 4 * tab_n + wave * n;
+  float* Ublk = smem + kWaves * 4 * tab_n + kWaves * n;
   const int64_t b = blockIdx.y;
   const float* Ub = U + b * C * C;
   if constexpr (LDSU) {
@@ -319,36 +329,46 @@ __global__ void __launch_bounds__(kWaves * 64)
     const float range = wmax - wmin;
     float best_err = 0.0f, s32 = 0.0f, b32 = 0.0f;
     for (int bt = 0; bt < n_batches; ++bt) {
-      // lane l prepares candidate 64 bt + l: scale, bias, divisor reciprocal
-      const int cl = 64 * bt + lane < sh.n ? 64 * bt + lane : sh.n - 1;
-      const float sc_l = round_to_storage(range * sh.p_over_maxq[cl], storage);
-      const float bi_l = round_to_storage(wmin * sh.p[cl], storage);
-      const float ss_l = (fabsf(sc_l) < 1e-12f) ? 1.0f : sc_l;
-      const float ys_l = div_exact_recip(ss_l);
+      // lane l prepares candidate 64 bt + l: scale, bias, divisor and its
+      // reciprocal, into the wave's table (one LDS read per candidate)
+      {
+        const int cl = 64 * bt + lane < sh.n ? 64 * bt + lane : sh.n - 1;
+        const float sc_l = round_to_storage(range * sh.p_over_maxq[cl], storage);
+        const float bi_l = round_to_storage(wmin * sh.p[cl], storage);
+        const float ss_l = (fabsf(sc_l) < 1e-12f) ? 1.0f : sc_l;
+        ctab[lane] = float4{sc_l, bi_l, ss_l, div_exact_recip(ss_l)};
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
       // candidates kCand at a time, their error sums reduced in one
       // butterfly; slots past the batch score a copy of its last candidate
       // (an equal error never replaces the earlier best under strict '<').
-      // The quotients of the whole batch take the exact-division correction,
-      // with one wave-uniform test for the rare operands outside its range.
+      // The quotients of the whole batch take the exact-division correction;
+      // the numerators' magnitudes (as in the column chain) and a zero
+      // reciprocal send the batch's out-of-range quotients to the IEEE
+      // division.
       const int nb = sh.n - 64 * bt < 64 ? sh.n - 64 * bt : 64;
       for (int c0 = 0; c0 < nb; c0 += kCand) {
         float sc[kCand], bi[kCand], ss[kCand], ys[kCand], part[kCand];
         float num[kCand][CPL], quo[kCand][CPL];
-        bool slow = false;
+        uint32_t mag_lo = 0xffffffffu;
+        float mag_hi = 0.0f;
+        bool y_zero = false;
 #pragma unroll
         for (int i = 0; i < kCand; ++i) {
           const int ci = c0 + i < nb ? c0 + i : nb - 1;
-          sc[i] = lane_read(sc_l, ci);
-          bi[i] = lane_read(bi_l, ci);
-          ss[i] = lane_read(ss_l, ci);
-          ys[i] = lane_read(ys_l, ci);
+          const float4 pc = ctab[ci];
+          sc[i] = pc.x, bi[i] = pc.y, ss[i] = pc.z, ys[i] = pc.w;
+          y_zero |= !(ys[i] != 0.0f);
 #pragma unroll
           for (int s = 0; s < CPL; ++s) {
             num[i][s] = acc[s] - bi[i];
             quo[i][s] = div_fast(num[i][s], ss[i], ys[i]);
-            slow |= act[s] & div_slow(num[i][s], ys[i]);
+            mag_lo = min(mag_lo, (f2u(num[i][s]) << 1) - 2u);
+            mag_hi = fmaxf(mag_hi, fabsf(num[i][s]));
           }
         }
+        const bool slow = y_zero | (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f);
         if (__builtin_amdgcn_ballot_w64(slow) != 0) {
           asm volatile("" ::: "memory");
 #pragma unroll
@@ -362,16 +382,19 @@ __global__ void __launch_bounds__(kWaves * 64)
           part[i] = 0.0f;
 #pragma unroll
           for (int s = 0; s < CPL; ++s) {
-            const float qt = num[i][s] == 0.0f ? num[i][s] : quo[i][s];
+            // a zero numerator's quotient is that zero (see the column chain)
+            const float qt = copysignf(quo[i][s], num[i][s]);
             const float d = affine_round(qt, maxq) * sc[i] + bi[i] - acc[s];
             part[i] = act[s] ? part[i] + d * d : part[i];
           }
         }
-        wave_sum_n<kCand>(part);
+        float sums[kCand / 4];
+        wave_sum_halving<kCand>(part, sums);
 #pragma unroll
         for (int i = 0; i < kCand; ++i) {
-          if ((bt == 0 && c0 + i == 0) || part[i] < best_err) {
-            best_err = part[i];
+          const float pi = lane_read(sums[i % (kCand / 4)], 16 * (i / (kCand / 4)));
+          if ((bt == 0 && c0 + i == 0) || pi < best_err) {
+            best_err = pi;
             s32 = sc[i];
             b32 = bi[i];
           }
@@ -699,7 +722,8 @@ extern "C" int mgq_gptq_affine_block(float* W, const float* U, int64_t B, int64_
   const dim3 blocks(static_cast<unsigned>(ceil_div(R, kWaves)), static_cast<unsigned>(B));
   const float maxq = static_cast<float>((1 << bits) - 1);
   const bool ldsu = n <= kLdsBlock;
-  const size_t lds = sizeof(float) * (kWaves * 4 * static_cast<size_t>(group_size) +
+  const size_t tab_n = group_size > 64 ? group_size : 64;
+  const size_t lds = sizeof(float) * (kWaves * 4 * tab_n +
                                       kWaves * static_cast<size_t>(n) +
                                       (ldsu ? static_cast<size_t>(n) * n : 0));
 #define AFFINE_LAUNCH(CPL_, LDSU_)                                                          \
