@@ -382,9 +382,11 @@ __global__ void __launch_bounds__(kWaves * 64)
           part[i] = 0.0f;
 #pragma unroll
           for (int s = 0; s < CPL; ++s) {
-            // a zero numerator's quotient is that zero (see the column chain)
+            // a zero numerator's quotient is that zero (see the column chain);
+            // the clamp need not keep a NaN: a NaN quotient comes only from a
+            // NaN acc, which makes d NaN anyway
             const float qt = copysignf(quo[i][s], num[i][s]);
-            const float d = affine_round(qt, maxq) * sc[i] + bi[i] - acc[s];
+            const float d = fminf(fmaxf(rintf(qt), 0.0f), maxq) * sc[i] + bi[i] - acc[s];
             part[i] = act[s] ? part[i] + d * d : part[i];
           }
         }
@@ -474,8 +476,12 @@ __global__ void __launch_bounds__(kWaves * 64)
         } else {
           // a zero numerator's quotient is that zero: copysign turns the
           // correction's +0 into it (every other quotient has its sign)
+          // NaN is not kept here: a NaN quotient means a NaN column value,
+          // which reaches wn at the end of the group and sends the group to
+          // the exact pass, whose rounding keeps it
           const float n1 = wn - b32;
-          const float q = affine_round(copysignf(div_fast(n1, s_safe, ysafe), n1), maxq);
+          const float q =
+              fminf(fmaxf(rintf(copysignf(div_fast(n1, s_safe, ysafe), n1)), 0.0f), maxq);
           const float dq = q * s32 + b32;
           const float n2 = wn - dq;
           e = copysignf(div_fast(n2, diag, ydg), n2);
@@ -487,8 +493,9 @@ __global__ void __launch_bounds__(kWaves * 64)
         wn = pre1 - e * u1;
       };
       // Row c of the group's U block at urow + c * ust. Rows arrive eight
-      // columns ahead; the last eight full columns load nothing, and the
-      // columns past the last multiple of 8 load their own rows.
+      // columns ahead (a slot is refilled once its column is done); the last
+      // eight full columns load nothing, and the columns past the last
+      // multiple of 8 load their own rows.
       const float* urow = LDSU ? Ublk + (j - i1) * n + (j - i1) : Ub + j * C + j;
       const int64_t ust = LDSU ? n : C;
       // (lanes past the group read the row's first entry: their values are
@@ -506,12 +513,9 @@ __global__ void __launch_bounds__(kWaves * 64)
       for (; c0 + 8 < G8; c0 += 8) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          float uc[CPL];
-#pragma unroll
-          for (int s = 0; s < CPL; ++s) uc[s] = ring[u][s];
+          column(c0 + u, c0 + u + 1, ring[u]);
           load_row(unext, ring[u]);
           unext += ust;
-          column(c0 + u, c0 + u + 1, uc);
         }
       }
       if (G8 > 0) {
@@ -526,9 +530,9 @@ __global__ void __launch_bounds__(kWaves * 64)
         load_row(urow + c * ust, uc);
         column(c, c + 1 < G ? c + 1 : c, uc);
       }
-      // nonzero numerators below 2^-100, or any at or above 2^101 (NaN
-      // quotients are NaN either way)
-      return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f);
+      // nonzero numerators below 2^-100, any at or above 2^101, or a NaN
+      // anywhere in the chain (it reaches the final wn through e)
+      return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f) | (wn != wn);
     };
     // every lane computed the same chain, so its verdict is wave-uniform
     if (y_zero || __builtin_amdgcn_ballot_w64(run_columns(std::false_type{})) != 0) {
