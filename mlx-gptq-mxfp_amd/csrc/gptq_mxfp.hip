@@ -365,6 +365,7 @@ __global__ void __launch_bounds__(kThreads)
   __shared__ float Ut[kG * kG];
   // RN(1/U[c][c]) for the correctly rounded divisions of the recurrence
   __shared__ float ydiag[kG];
+  __shared__ int ydiag_zero_s;
   // the safe search's objective operand: Hg as three exact bf16 parts
   HSplit* hs = nullptr;
   if constexpr (SAFE) {
@@ -374,10 +375,18 @@ __global__ void __launch_bounds__(kThreads)
   {
     const float* Ub = U + (b * G + g) * kG * kG;
     for (int e = threadIdx.x; e < kG * kG; e += kThreads) Ut[(e % kG) * kG + e / kG] = Ub[e];
-    if (threadIdx.x < kG) ydiag[threadIdx.x] = div_exact_recip(Ub[threadIdx.x * (kG + 1)]);
+    // wave 0 also records whether any reciprocal is 0 (a divisor outside
+    // [2^-24, 2^24]), for the whole workgroup
+    const float yv = threadIdx.x < kG ? div_exact_recip(Ub[threadIdx.x * (kG + 1)]) : 1.0f;
+    if (threadIdx.x < kG) ydiag[threadIdx.x] = yv;
+    if (threadIdx.x < 64) {
+      const bool z = __builtin_amdgcn_ballot_w64(!(yv != 0.0f)) != 0;
+      if (threadIdx.x == 0) ydiag_zero_s = z ? 1 : 0;
+    }
     if constexpr (SAFE) stage_hsplit(Hg, hs);
   }
   __syncthreads();
+  const bool ydiag_zero = ydiag_zero_s != 0;
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
   const int64_t base = (b * R + r) * C + g * kG;
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
@@ -493,27 +502,53 @@ __global__ void __launch_bounds__(kThreads)
   // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
   // Forming w_c lazily from the stored errors performs exactly those
   // roundings while keeping only err[] live.
+  //
+  // The divisions take Markstein's correction without a branch (EXACT =
+  // false; copysign gives a zero numerator its own zero) and only record the
+  // numerators' range: their smallest nonzero magnitude (as a bit pattern
+  // shifted left by one, minus 2, so that a zero wraps to the top) and their
+  // largest. If one fell outside the correction's exact range, or a NaN
+  // appeared (it reaches the last error through every later column), the
+  // wave runs the recurrence again with div_exact (EXACT = true); a divisor
+  // outside [2^-24, 2^24] (ydiag 0) sends the workgroup there directly.
   float errs[kG];
+  auto recurrence = [&](auto exact_tag) __attribute__((always_inline)) -> bool {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+    uint32_t mag_lo = 0xffffffffu;
+    float mag_hi = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
+    for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
 #pragma unroll
-  for (int c = 0; c < kG; ++c) {
-    // column c of U (row c of Ut, 16-byte aligned), read 4 values at a time
-    const lds_f32* col = (const lds_f32*)Ut + c * kG;
-    if (c) col = lds_after(col, errs[c - 1]);
-    float acc = ORIG(c);
+    for (int c = 0; c < kG; ++c) {
+      // column c of U (row c of Ut, 16-byte aligned), read 4 values at a time
+      const lds_f32* col = (const lds_f32*)Ut + c * kG;
+      if (c) col = lds_after(col, errs[c - 1]);
+      float acc = ORIG(c);
 #pragma unroll
-    for (int k0 = 0; k0 < c; k0 += 4) {
-      const f32x4_t u4 = *reinterpret_cast<const lds_f32x4*>(col + k0);
+      for (int k0 = 0; k0 < c; k0 += 4) {
+        const f32x4_t u4 = *reinterpret_cast<const lds_f32x4*>(col + k0);
 #pragma unroll
-      for (int k = k0; k < c && k < k0 + 4; ++k) acc = acc - errs[k] * u4[k - k0];
+        for (int k = k0; k < c && k < k0 + 4; ++k) acc = acc - errs[k] * u4[k - k0];
+      }
+      float dq;
+      const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
+      const float a = acc - dq;  // errs[c] = a / U[c][c]
+      if constexpr (EXACT) {
+        errs[c] = div_exact(a, col[c], ydiag[c]);
+      } else {
+        const float y = ydiag[c], q = a * y;
+        errs[c] = copysignf(fmaf(fmaf(-q, col[c], a), y, q), a);
+        mag_lo = min(mag_lo, (f2u(a) << 1) - 2u);
+        mag_hi = fmaxf(mag_hi, fabsf(a));
+      }
+      codes[c / 4] |= code << (8 * (c % 4));
+      dq_set(c, dq);
     }
-    float dq;
-    const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
-    errs[c] = div_exact(acc - dq, col[c], ydiag[c]);  // = (acc - dq) / U[c][c]
-    codes[c / 4] |= code << (8 * (c % 4));
-    dq_set(c, dq);
-  }
+    return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f) |
+           (errs[kG - 1] != errs[kG - 1]);
+  };
+  if (ydiag_zero || __builtin_amdgcn_ballot_w64(recurrence(std::false_type{})) != 0)
+    recurrence(std::true_type{});
 
   // 3. GPTQ vs best RTN candidate (safe search only)
   bool use_gptq = true;
