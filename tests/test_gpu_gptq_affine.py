@@ -129,6 +129,38 @@ def test_affine_out_of_range_operands_vs_oracle(case, w_mult, h_mult):
     _check_vs(W, q, s, b, W_dq, rq, rs, rb, rW, Hr)
 
 
+def test_affine_nonfinite_weights_leave_other_rows_on_the_oracle():
+    """NaN and inf weights: a row's errors only reach that row's later
+    columns, so every other row must still match the oracle. The column loop
+    sends a group whose chain met a NaN or an infinity to its exact pass, and
+    the clip search's ranges must not be thrown off for the rest."""
+    from mlx_gptq import grid, gptq
+
+    W, H, _ = _setup(B=2, R=64, C=256, N=1024, seed=13, scale=0.02)
+    W[0, 3, 70] = float("nan")
+    W[1, 10, 5] = float("inf")
+    W[1, 11, 127] = -float("inf")
+    W[0, 50, 200:210] = float("nan")
+    Wg, Hg = W.clone().to(DEV), H.clone().to(DEV)
+    q, s, b, W_dq, _ = gptq.gptq_quantize(Wg, Hg, 4, 64, storage_dtype=torch.float32)
+    Wr, Hr = W.clone(), H.clone()
+    rq, rs, rb, rW, _ = gptq_ref.gptq_quantize(Wr, Hr, 4, 64, storage_dtype=torch.float32)
+    good = torch.isfinite(W).all(dim=-1)  # [B, R]
+    assert int((~good).sum()) == 4
+    q, s, b, W_dq = q.cpu(), s.cpu(), b.cpu(), W_dq.cpu()
+    assert int(q.max()) <= 15
+    assert _agree(q[good], rq[good]) >= 0.995
+    assert torch.allclose(s[good], rs[good], rtol=1e-4, atol=0)
+    assert torch.allclose(b[good], rb[good], rtol=1e-4, atol=1e-7)
+    dec = grid.dequantize_artifact(q, s, b, "affine", 64)
+    assert torch.equal(dec[good], W_dq[good])
+    for i in range(2):
+        rows = good[i]
+        pl = gptq_ref.proxy_loss(W[i, rows][None], W_dq[i, rows][None], Hr[i][None])
+        pl_ref = gptq_ref.proxy_loss(W[i, rows][None], rW[i, rows][None], Hr[i][None])
+        assert torch.isfinite(pl).all() and (pl - pl_ref).abs() <= 0.01 * pl_ref.abs()
+
+
 def test_affine_config1_shape_vs_oracle():
     """BASELINE config 1 (single Linear 2048x2048, affine 4-bit, G=64, block
     128, MSE clip) at its real size, on 8192 lognormal tokens with 1% x20

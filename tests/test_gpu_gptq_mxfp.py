@@ -88,6 +88,34 @@ def test_mxfp_matches_oracle_larger(mode, alg):
     assert torch.all((pl - pl_ref).abs() <= 0.01 * pl_ref.abs()), (pl, pl_ref)
 
 
+@pytest.mark.parametrize("mode,alg", [("mxfp4", "safe-scale-search"), ("mxfp8", "groupwise")])
+def test_mxfp_nonfinite_weights_leave_other_groups_on_the_oracle(mode, alg):
+    """NaN and inf weights stay inside their own (row, 32-column group): the
+    recurrence's fast divisions send a wave that met one to its exact pass,
+    and every other group must still match the oracle."""
+    from mlx_gptq import grid, gptq
+
+    W, H, _ = _setup(B=3, R=64, C=256, N=2048, seed=9, scale=0.02)
+    W[0, 3, 70] = float("nan")
+    W[1, 10, 5:9] = float("inf")
+    W[2, 7, 100] = -float("inf")
+    W[2, 8, 0] = float("nan")
+    bits = 4 if mode == "mxfp4" else 8
+    Hg = H.clone().to(DEV)
+    q, s, _, W_dq, _ = gptq.solve_gptq(W.to(DEV), Hg, bits, 32, mode=mode, mxfp_algorithm=alg)
+    rq, rs, _, rW, _ = gptq_ref.solve_gptq(W.clone(), H.clone(), bits, 32, mode=mode,
+                                           mxfp_algorithm=alg)
+    B, R, C = W.shape
+    good_g = torch.isfinite(W).view(B, R, C // 32, 32).all(dim=-1)  # [B, R, C/32]
+    good = good_g.repeat_interleave(32, dim=-1)
+    assert int((~good_g).sum()) == 4
+    q, s, W_dq = q.cpu(), s.cpu(), W_dq.cpu()
+    assert _agree(q[good], rq[good]) >= 0.995
+    assert _agree(s[good_g], rs[good_g]) >= (1.0 if alg == "groupwise" else 0.99)
+    assert torch.equal(grid.dequantize_artifact(q, s, None, mode, 32)[good], W_dq[good])
+    assert torch.isfinite(W_dq[good]).all()
+
+
 def test_prepare_hinv_blocks_vs_oracle():
     from mlx_gptq import gptq
 
