@@ -408,21 +408,31 @@ __global__ void __launch_bounds__(kThreads)
     const uint4 m0 = reinterpret_cast<const uint4*>(dd)[0];
     const uint4 m1 = reinterpret_cast<const uint4*>(dd)[1];
     const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    const bool any_dead = (m0.x | m0.y | m0.z | m0.w | m1.x | m1.y | m1.z | m1.w) != 0u;  // uniform
     if (rel_part) {
 #pragma unroll
       for (int i = 0; i < kG; ++i) den = fmaf(v[i], v[i], den);
-      if ((m0.x | m0.y | m0.z | m0.w | m1.x | m1.y | m1.z | m1.w) != 0u) {  // uniform
+      if (any_dead) {
 #pragma unroll
         for (int i = 0; i < kG; ++i)
           if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) dead_sq = fmaf(v[i], v[i], dead_sq);
       }
     }
+    if (any_dead) {
 #pragma unroll
-    for (int i = 0; i < kG; ++i)
-      if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) v[i] = 0.0f;
-    amax = fabsf(v[0]);
+      for (int i = 0; i < kG; ++i)
+        if ((mw[i / 4] >> (8 * (i % 4))) & 0xffu) v[i] = 0.0f;
+    }
+    // amax = max |v|, NaN when any v is NaN (grid.py's amax propagates it;
+    // which NaN does not matter: e8m0_exponent and the range guard only
+    // test for one). Magnitudes order like their bit patterns, NaN above
+    // infinity, so an unsigned max of the patterns gives exactly that.
+    {
+      uint32_t mb = 0u;
 #pragma unroll
-    for (int i = 1; i < kG; ++i) amax = nan_max(amax, fabsf(v[i]));
+      for (int i = 0; i < kG; ++i) mb = max(mb, f2u(v[i]) & 0x7fffffffu);
+      amax = __uint_as_float(mb);
+    }
 #pragma unroll
     for (int p = 0; p < kG / 2; ++p)
       *reinterpret_cast<float2*>(so + p * 2 * kThreads + 2 * threadIdx.x) = make_float2(v[2 * p], v[2 * p + 1]);
