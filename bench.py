@@ -129,21 +129,34 @@ def _copy_calibration(torch, dev, mib):
     del src, dst
 
 
+def _events(torch, n):
+    """A step's own timing events (steps run back to back, so each needs its own)."""
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
 def _timed(torch, np, step, n_phase, warmup, steps):
+    """Warmup, then exactly `steps` steps between two device synchronizations
+    (the host queues step i+1 while the GPU runs step i, as a layer-by-layer
+    driver would). Phase times and the per-step median come from each step's
+    own events, read after the closing synchronization: a step's first event
+    completes when the previous step's work has, so its span is that step's
+    time on the GPU."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     phase = np.zeros(n_phase)
-    per_step = []
-    t0 = time.perf_counter()
     out = None
+    all_evs = []
+    t0 = time.perf_counter()
     for _ in range(steps):
-        ts = time.perf_counter()
         out, evs = step()
-        torch.cuda.synchronize()  # events of this step are complete
-        per_step.append((time.perf_counter() - ts) * 1e3)
-        phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(n_phase)]
+        all_evs.append(evs)
+    torch.cuda.synchronize()
     t1 = time.perf_counter()
+    per_step = []
+    for evs in all_evs:
+        phase += [evs[i].elapsed_time(evs[i + 1]) for i in range(n_phase)]
+        per_step.append(evs[0].elapsed_time(evs[n_phase]))
     _timed.median_ms = float(np.median(per_step)) if per_step else 0.0
     return out, (t1 - t0) * 1e3 / steps, phase / steps
 
@@ -194,9 +207,8 @@ def run_moe(args, torch, np) -> int:
 
     H_gu = torch.empty(E, hidden, hidden, dtype=torch.float32, device=dev)
     H_dn = torch.empty(E, inter, inter, dtype=torch.float32, device=dev)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-
     def step():
+        evs = _events(torch, 6)
         evs[0].record()
         capture.grouped_hessian(L.X, L.offsets, L.row_index, out=H_gu, validate=False)
         evs[1].record()
@@ -262,10 +274,10 @@ def run_capture(args, torch, np) -> int:
     H = torch.empty(E, hidden, hidden, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     stash = capture.RoutedStash("gate_up", hidden, E)
 
     def step():
+        evs = _events(torch, 4)
         stash.clear()
         evs[0].record()
         for a, b in batches:
@@ -348,9 +360,8 @@ def run_audit(args, torch, np) -> int:
     del L
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-
     def step():
+        evs = _events(torch, 2)
         evs[0].record()
         st = validate_artifacts.range_audit(src, q, sb, None, "mxfp4", 32)
         evs[1].record()
@@ -531,9 +542,8 @@ def run_dense(args, torch, np) -> int:
         stashes[k] = st
     torch.cuda.synchronize()
     n_ev = len(keys) + len(L.mats) + 1
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev + 1)]
-
     def step():
+        evs = _events(torch, n_ev + 1)
         i = 0
         evs[i].record()
         Hs = {}

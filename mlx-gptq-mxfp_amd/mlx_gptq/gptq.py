@@ -286,10 +286,21 @@ def solve_gptq(
     from . import gptq_affine
 
     W0, H_d = _staged(W_orig, H)
+    assert W0.dim() == 3 and H_d.dim() == 3
+    B, R, C = W0.shape
+    assert H_d.shape == (B, C, C)
+    assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
+    # W is a private copy, so the column loop may start before the first
+    # damped pass is known to have succeeded; if it had not, solve again from
+    # a fresh copy on the synchronous path (escalation, warnings, errors)
     W = W0.float().clone()
-    q, s, b, W_dq, _ = gptq_quantize(W, H_d, bits, group_size, damp=damp, clip=clip,
-                                     storage_dtype=storage_dtype, mode=mode,
-                                     mxfp_algorithm=mxfp_algorithm)
+    res = gptq_affine.gptq_quantize_affine(W, H_d, bits, group_size, damp, clip, storage_dtype,
+                                           128, speculative=True)
+    if res is None:
+        W = W0.float().clone()
+        res = gptq_quantize(W, H_d, bits, group_size, damp=damp, clip=clip,
+                            storage_dtype=storage_dtype, mode=mode, mxfp_algorithm=mxfp_algorithm)
+    q, s, b, W_dq, _ = res
     rel = gptq_affine.rel_err(W_dq, W0)
     if H_d is not H:
         H.copy_(H_d)

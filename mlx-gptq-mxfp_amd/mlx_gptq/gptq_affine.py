@@ -45,8 +45,14 @@ def prepare_hinv_full(H: torch.Tensor, damp: float, max_attempts: int):
     cur = np.full(B, np.float32(damp), dtype=np.float32)
     active = np.ones(B, dtype=bool)
     for att in range(1, int(max_attempts) + 1):
-        damp_d = torch.from_numpy(cur).to(dev)
-        active_d = torch.from_numpy(active.astype(np.uint8)).to(dev)
+        if att == 1:
+            # every item, one damp: filled on the device (a host-to-device copy
+            # from pageable memory would hold the host until the stream drains)
+            damp_d = torch.full((B,), float(cur[0]), dtype=torch.float32, device=dev)
+            active_d = torch.ones(B, dtype=torch.uint8, device=dev)
+        else:
+            damp_d = torch.from_numpy(cur).to(dev)
+            active_d = torch.from_numpy(active.astype(np.uint8)).to(dev)
         failed_d = torch.zeros(B, dtype=torch.uint8, device=dev)
         nat.call("mgq_hinv_full_pass", H.data_ptr(), B, C, damp_d.data_ptr(), active_d.data_ptr(),
                  failed_d.data_ptr(), U.data_ptr(), ws.data_ptr(), ws.numel(), stream)
@@ -59,11 +65,42 @@ def prepare_hinv_full(H: torch.Tensor, damp: float, max_attempts: int):
     return U, attempts
 
 
+def _first_pass_async(H: torch.Tensor, damp: float):
+    """The first damped pass of prepare_hinv_full with every item active, its
+    per-item failure flags copied to pinned host memory without waiting.
+    Returns (U, flags, event): the flags are valid once the event has
+    completed; U holds the factor of every item whose flag is 0."""
+    B, C, _ = H.shape
+    dev = H.device
+    lib = nat.load()
+    stream = nat.stream_of(dev)
+    U = torch.empty(B, C, C, dtype=torch.float32, device=dev)
+    ws = torch.empty(int(lib.mgq_hinv_full_workspace_size(B, C)), dtype=torch.uint8, device=dev)
+    damp_d = torch.full((B,), float(np.float32(damp)), dtype=torch.float32, device=dev)
+    active_d = torch.ones(B, dtype=torch.uint8, device=dev)
+    failed_d = torch.zeros(B, dtype=torch.uint8, device=dev)
+    nat.call("mgq_hinv_full_pass", H.data_ptr(), B, C, damp_d.data_ptr(), active_d.data_ptr(),
+             failed_d.data_ptr(), U.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    flags = torch.empty(B, dtype=torch.uint8, pin_memory=True)
+    flags.copy_(failed_d, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(dev))
+    return U, flags, ev
+
+
 def gptq_quantize_affine(W: torch.Tensor, H: torch.Tensor, bits: int, group_size: int,
-                         damp: float, clip: str, storage_dtype: torch.dtype, block_size: int):
+                         damp: float, clip: str, storage_dtype: torch.dtype, block_size: int,
+                         speculative: bool = False):
     """gptq.py:216-272 for mode "affine". W f32 [B, R, C] becomes W_dq in place;
     H f32 [B, C, C] gets the dead-column diagonal fix in place.
-    Returns (q u8 [B,R,C], scales, biases [B,R,C/G] storage_dtype, W, None)."""
+    Returns (q u8 [B,R,C], scales, biases [B,R,C/G] storage_dtype, W, None).
+
+    speculative: the column loop is launched right after the first damped
+    pass, without waiting for its failure flags; they are read once every
+    launch is queued. If some item failed, None is returned and W holds no
+    meaningful result: the caller solves again from its own copy of W on the
+    synchronous path, which escalates the damping and reports as the
+    reference does. For callers whose W is a private copy (solve_gptq)."""
     from .gptq import _prepare_hinv, _require_device
 
     if W.dtype != torch.float32:
@@ -80,7 +117,11 @@ def gptq_quantize_affine(W: torch.Tensor, H: torch.Tensor, bits: int, group_size
     dev = W.device
     stream = nat.stream_of(dev)
     nat.call("mgq_dead_fix", W.data_ptr(), B, R, C, H.data_ptr(), stream)
-    U = _prepare_hinv(H, damp)
+    if speculative and C != 32 and B * R * C > 0:
+        U, flags, ev = _first_pass_async(H, damp)
+    else:
+        speculative = False
+        U = _prepare_hinv(H, damp)
 
     bs = max(int(block_size), G)
     bs -= bs % G
@@ -97,4 +138,8 @@ def gptq_quantize_affine(W: torch.Tensor, H: torch.Tensor, bits: int, group_size
         nat.call("mgq_gptq_affine_block", W.data_ptr(), U.data_ptr(), B, R, C, i1, n, G, bits,
                  method, storage, 20, 0.2, q_out.data_ptr(), scales.data_ptr(),
                  biases.data_ptr(), Err.data_ptr(), stream)
+    if speculative:
+        ev.synchronize()  # the first pass's flags (the blocks keep running)
+        if bool(flags.any()):
+            return None
     return q_out, scales, biases, W, None

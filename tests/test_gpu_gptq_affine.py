@@ -269,6 +269,57 @@ def test_full_escalation_warnings_match_oracle(caplog):
     assert [r.getMessage() for r in caplog.records] == ref_msgs
 
 
+def test_solve_falls_back_when_the_first_damped_pass_fails(caplog):
+    """solve_gptq launches the affine column loop before it knows the first
+    damped pass succeeded. When an item needs more damping, it must solve
+    again on the synchronous path: the outputs are those of gptq_quantize on
+    a copy of W, with the reference's warnings; an item that never factors
+    raises the reference's RuntimeError."""
+    from mlx_gptq import gptq
+
+    def coupled(B, C, off):
+        # SPD items with a positive diagonal (so the dead-column fix keeps
+        # them) and entries (5, 6), (6, 5) set to off[i]: the 2x2 block
+        # [[1, o], [o, 1]] needs a damping above o - 1 to factor
+        gg = torch.Generator().manual_seed(23)
+        Hc = torch.zeros(B, C, C)
+        for i in range(B):
+            A = torch.randn(C, C, generator=gg) * 0.01
+            Hc[i] = A @ A.T + torch.eye(C)
+            if off[i] is not None:
+                Hc[i, 5, 6] = Hc[i, 6, 5] = off[i]
+        return Hc
+
+    C = 128
+    H = coupled(3, C, [None, 1.05, 3.0])  # needs damp 0.1 and 10
+    g = torch.Generator().manual_seed(31)
+    W = torch.randn(3, 48, C, generator=g) * 0.02
+    with caplog.at_level(logging.WARNING, logger="mlx_gptq.gptq"):
+        q, s, b, W_dq, rel = gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), 4, 64)
+    msgs = [r.getMessage() for r in caplog.records]
+    caplog.clear()
+    with caplog.at_level(logging.WARNING, logger="mlx_gptq.gptq"):
+        Wc = W.clone().to(DEV)
+        q2, s2, b2, W2, _ = gptq.gptq_quantize(Wc, H.clone().to(DEV), 4, 64)
+    assert msgs == [r.getMessage() for r in caplog.records] and len(msgs) >= 2
+    assert torch.equal(q, q2) and torch.equal(s, s2) and torch.equal(b, b2)
+    assert torch.equal(W_dq, W2)
+    assert torch.isfinite(rel).all()
+
+    Hf = coupled(3, C, [None, 1e6, None])  # item 1 never factors
+    caplog.clear()
+    with caplog.at_level(logging.WARNING, logger="oracle.gptq_ref"):
+        with pytest.raises(RuntimeError) as ei_ref:
+            gptq_ref.prepare_hinv(Hf.clone(), 0.01)
+    ref_msgs = [r.getMessage() for r in caplog.records]
+    caplog.clear()
+    with caplog.at_level(logging.WARNING, logger="mlx_gptq.gptq"):
+        with pytest.raises(RuntimeError) as ei:
+            gptq.solve_gptq(W.to(DEV), Hf.clone().to(DEV), 4, 64)
+    assert str(ei.value) == str(ei_ref.value)
+    assert [r.getMessage() for r in caplog.records] == ref_msgs
+
+
 def test_affine_batched_equals_per_item():
     """Reference tests/test_gptq.py:44-52 (bit-exact), affine mode."""
     from mlx_gptq import gptq
