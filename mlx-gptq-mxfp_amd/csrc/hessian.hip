@@ -6,7 +6,9 @@
 // token t reads row `row_index ? row_index[t] : t` of X, so the routed-expert
 // gather is fused into the tile loads. Only the lower triangle of 256x256
 // output tiles is computed; each tile is mirrored on store, so H is exactly
-// symmetric.
+// symmetric. Diagonal tiles go in pairs: one workgroup computes the lower
+// triangles of two of them, which costs it about what one off-diagonal tile
+// costs (the same bytes per token, 18 MFMAs per K-step against 16).
 //
 // Tile kernel (512 threads = 8 waves, two per SIMD, 1 workgroup per CU):
 //   - output tile 256x256, each wave 128x64 = 4x2 blocks of
@@ -74,70 +76,103 @@ inline int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; 
 // A row of C bf16 zeros that tail tokens (past a work item's range) load.
 inline int64_t zero_row_bytes(int64_t C) { return align_up(2 * C); }
 
-// Flush the wave's 128x128 accumulators into `out` (row stride ld). Direct
-// tiles (H_g, global coordinates) keep the lower triangle and
-// mirror it; partial tiles (local 256x256 slot) are stored whole. Offsets are
-// 32-bit (C*C < 2^31 is checked on the host) and the stride is kept in a
-// VGPR so the 64 row offsets are formed per element instead of occupying
-// scalar registers.
-template <int NA>
-__device__ inline void flush(f32x16_t (&acc)[4][NA], float* __restrict__ out, uint32_t ld_s,
-                             bool direct, bool add, uint32_t C, uint32_t gi0, uint32_t gj0,
-                             int lane, bool interior) {
+// MFMA j of a K-step and the fragments it takes, numbered in the order the
+// K-step reads them:
+//   - 8 MFMAs (a 128x64 part, 4x2 blocks): reads a0 b0 b1 a1 a2 a3, MFMA j is
+//     block (j / 2, j % 2);
+//   - 10 MFMAs (the lower triangle of a 128x128 diagonal part): reads F0..F3,
+//     the four 32-channel blocks, each of them both an A and a B operand;
+//     MFMA j is block (r, c), c <= r, row by row.
+constexpr int tri_row(int j) { return j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3; }
+constexpr int tri_col(int j) { return j - tri_row(j) * (tri_row(j) + 1) / 2; }
+template <int NM>
+constexpr int op_a(int j) {
+  return NM == 8 ? ((j >> 1) == 0 ? 0 : (j >> 1) + 2) : tri_row(j);
+}
+template <int NM>
+constexpr int op_b(int j) {
+  return NM == 8 ? 1 + (j & 1) : tri_col(j);
+}
+
+// The stride is kept in a VGPR so the row offsets are formed per element
+// instead of occupying scalar registers.
+__device__ inline uint32_t ld_vgpr(uint32_t ld_s) {
   uint32_t ld;
   asm volatile("v_mov_b32 %0, %1" : "=v"(ld) : "s"(ld_s));
-  const uint32_t gj_l = gj0 + (lane & 31);
-  const uint32_t gi_l = gi0 + 4 * (lane >> 5);
-  if (interior) {
-    // Strictly-lower tile inside H: no masking. Registers 4q..4q+3 of a
-    // block hold rows gi..gi+3 of one column gj, so the mirrored values are
-    // 4 consecutive floats of row gj: one 16-byte store.
+  return ld;
+}
+
+// One 32x32 block at rows gi_l + 32 ma, columns gj (this lane's column). A
+// strictly-lower block inside H (whole) needs no masking: registers
+// 4q..4q+3 hold rows gi..gi+3 of column gj, so the mirrored values are 4
+// consecutive floats of row gj, one 16-byte store. Otherwise each entry is
+// kept if it lies in H's lower triangle (direct) and mirrored, or stored as
+// it is (a partial tile's slot).
+__device__ inline void flush_block(const f32x16_t& a, float* __restrict__ out, uint32_t ld,
+                                   bool whole, bool direct, bool add, uint32_t C, uint32_t gi_b,
+                                   uint32_t gj) {
+  if (whole) {
 #pragma unroll
-    for (int ma = 0; ma < 4; ++ma) {
+    for (int rq = 0; rq < 4; ++rq) {
+      const uint32_t gi = gi_b + 8 * rq;
+      float nv[4];
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const uint32_t gi = gi_l + ma * 32 + 8 * rq;
-#pragma unroll
-        for (int na = 0; na < NA; ++na) {
-          const uint32_t gj = gj_l + na * 32;
-          float nv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float* p = out + ((gi + e) * ld + gj);
-            const float v = acc[ma][na][4 * rq + e];
-            nv[e] = add ? (*p + v) : v;
-            *p = nv[e];
-          }
-          const float4 m = {nv[0], nv[1], nv[2], nv[3]};
-          *reinterpret_cast<float4*>(out + (gj * ld + gi)) = m;
-        }
+      for (int e = 0; e < 4; ++e) {
+        float* p = out + ((gi + e) * ld + gj);
+        nv[e] = add ? (*p + a[4 * rq + e]) : a[4 * rq + e];
+        *p = nv[e];
       }
+      *reinterpret_cast<float4*>(out + (gj * ld + gi)) = float4{nv[0], nv[1], nv[2], nv[3]};
     }
     return;
   }
 #pragma unroll
-  for (int ma = 0; ma < 4; ++ma) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t gi = gi_l + ma * 32 + 8 * (r >> 2) + (r & 3);
-      const uint32_t row_off = gi * ld;
-#pragma unroll
-      for (int na = 0; na < NA; ++na) {
-        const uint32_t gj = gj_l + na * 32;
-        const float v = acc[ma][na][r];
-        if (direct) {
-          if (gi < C && gj < C && gi >= gj) {
-            float* p = out + (row_off + gj);
-            const float nv = add ? (*p + v) : v;
-            *p = nv;
-            if (gi != gj) out[gj * ld + gi] = nv;
-          }
-        } else {
-          float* p = out + (row_off + gj);
-          *p = add ? (*p + v) : v;
-        }
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t gi = gi_b + 8 * (r >> 2) + (r & 3);
+    const float v = a[r];
+    float* p = out + (gi * ld + gj);
+    if (direct) {
+      if (gi < C && gj < C && gi >= gj) {
+        const float nv = add ? (*p + v) : v;
+        *p = nv;
+        if (gi != gj) out[gj * ld + gi] = nv;
       }
+    } else {
+      *p = add ? (*p + v) : v;
     }
+  }
+}
+
+// Flush a wave's 128x64 part (4x2 blocks) at rows gi0.., columns gj0.. of
+// `out` (row stride ld): direct parts (H_g, global coordinates) keep the lower
+// triangle and mirror it; partial tiles (local 256x256 slot) are stored whole.
+// interior: the part lies strictly below H's diagonal and inside H. Offsets
+// are 32-bit (C*C < 2^31 is checked on the host).
+__device__ inline void flush_part(f32x16_t (&acc)[8], float* __restrict__ out, uint32_t ld_s,
+                                  bool direct, bool add, uint32_t C, uint32_t gi0, uint32_t gj0,
+                                  int lane, bool interior) {
+  const uint32_t ld = ld_vgpr(ld_s);
+  const uint32_t gj_l = gj0 + (lane & 31);
+  const uint32_t gi_l = gi0 + 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    flush_block(acc[j], out, ld, interior, direct, add, C, gi_l + 32 * (j >> 1),
+                gj_l + 32 * (j & 1));
+}
+
+// Flush the lower triangle of a 128x128 diagonal part at rows and columns
+// base.. of H (direct only): its strictly-lower blocks inside H are stored
+// whole and mirrored, its diagonal blocks (and blocks crossing C) masked.
+__device__ inline void flush_tri(f32x16_t (&acc)[10], float* __restrict__ out, uint32_t ld_s,
+                                 bool add, uint32_t C, uint32_t base, int lane) {
+  const uint32_t ld = ld_vgpr(ld_s);
+  const uint32_t gj_l = base + (lane & 31);
+  const uint32_t gi_l = base + 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 10; ++j) {
+    const int r = tri_row(j), c = tri_col(j);
+    const bool whole = c < r && base + 32 * r + 32 <= C;
+    flush_block(acc[j], out, ld, whole, true, add, C, gi_l + 32 * r, gj_l + 32 * c);
   }
 }
 
@@ -202,19 +237,23 @@ __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
 // accepts a 1 KB request per ~16 cycles) leaves the matrix pipe to the other
 // wave's MFMAs; with one wave per SIMD (a 128x128 quarter each) the same
 // stall idled the pipe (measured 3-6 % slower, same results bit for bit).
+//
+// Diagonal tiles of direct launches. An item with ti <= tj is diagonal:
+// ti == tj one tile, ti < tj the pair of tiles (ti, ti) and (tj, tj), whose
+// channels the A and B halves of the LDS rows hold (a pair moves the same
+// 1 KB per token as an off-diagonal tile). Each diagonal tile is cut into
+// rows 128..255 x columns 0..127 (two 4x2 parts, as in an off-diagonal
+// tile) and the lower triangles of its two 128x128 diagonal blocks (10
+// blocks each, the four 32-channel fragments of a K-step serving as both
+// operands). Waves 0-3 take the parts of tile ti and waves 4-7 those of tj,
+// arranged so that each SIMD runs one 4x2 part and one triangle: 18 MFMAs per
+// K-step against 16 for an off-diagonal tile, for two tiles. A single
+// diagonal tile leaves waves 4-7 with their DMAs only (10 MFMAs per K-step on
+// the busiest SIMD).
 #define SYRK_MFMA(P, j)                                                                   \
-  acc[(j) >> 1][(j) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                        \
-      fa[P][(j) >> 1], fb[P][(j) & 1], acc[(j) >> 1][(j) & 1], 0, 0, 0)
-// fragment q of a K-step, in the order the MFMAs consume them: a0 b0 b1 a1 a2 a3
-#define SYRK_READ(P, q, b)                                                                \
-  do {                                                                                     \
-    if ((q) == 0)                                                                          \
-      fa[P][0] = tr_frag(lds3 + (b) + offA[0]);                                            \
-    else if ((q) <= 2)                                                                     \
-      fb[P][(q) - 1] = tr_frag(lds3 + (b) + offB[(q) - 1]);                                \
-    else                                                                                   \
-      fa[P][(q) - 2] = tr_frag(lds3 + (b) + offA[(q) - 2]);                                \
-  } while (0)
+  acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[P][op_a<NM>(j)], fr[P][op_b<NM>(j)], \
+                                                   acc[j], 0, 0, 0)
+#define SYRK_READ(P, qq, b) fr[P][qq] = tr_frag(lds3 + (b) + off[qq])
 
 template <bool GATHER, bool BIG, int KB, int NB>
 __global__ void __launch_bounds__(kThreads, 1)
@@ -240,14 +279,12 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 2, wc = wave & 3;
   const bool diag = it.ti == it.tj;
   const bool direct = it.slot < 0;
+  const bool dtile = direct && it.ti <= it.tj;  // one diagonal tile or a pair
   float* out = direct ? H + static_cast<int64_t>(it.g) * C * C
                       : partials + static_cast<int64_t>(it.slot) * kTile * kTile;
   const uint32_t ld = direct ? static_cast<uint32_t>(C) : kTile;
-  const uint32_t gi0 = (direct ? static_cast<uint32_t>(it.ti) * kTile : 0u) + wr * 128;
-  const uint32_t gj0 = (direct ? static_cast<uint32_t>(it.tj) * kTile : 0u) + wc * 64;
 
   const int half = lane >> 5;
   const int64_t tile_ch = static_cast<int64_t>(half && !diag ? it.tj : it.ti) * kTile;
@@ -260,22 +297,13 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int g = lane >> 4, j4 = (lane >> 2) & 3, q = lane & 3;
   const uint32_t rd_lo = static_cast<uint32_t>((8 * (g >> 1) + j4) * kTokB + (g & 1) * 32 +
                                                (q >> 1) * 16 + (q & 1) * 8);
-  uint32_t offA[4], offB[2];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) offA[m] = rd_lo + wr * 256 + (m ^ j4) * 64;
-#pragma unroll
-  for (int n = 0; n < 2; ++n) offB[n] = rd_lo + 512 + ((2 * wc + n) ^ j4) * 64;
+  // fragment of 32-channel block m (0..7) of LDS half h
+  auto frag_off = [&](int h, int m) -> uint32_t {
+    return rd_lo + static_cast<uint32_t>(h * 512 + (m ^ j4) * 64);
+  };
   const lds_char_t* lds3 = (const lds_char_t*)lds;
   const uint32_t lds_u32 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds3));
   const uint32_t wave_dst = wave * kDmaWave * kTokB;
-
-  f32x16_t acc[4][2];
-#pragma unroll
-  for (int ma = 0; ma < 4; ++ma)
-#pragma unroll
-    for (int na = 0; na < 2; ++na)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[ma][na][r] = 0.0f;
 
   const char* Xb = reinterpret_cast<const char*>(X);
   const char* zr = reinterpret_cast<const char*>(zero_row);
@@ -323,31 +351,34 @@ __global__ void __launch_bounds__(kThreads, 1)
   auto stage_base = [&](int64_t t0) -> const char* {
     return Xb + static_cast<uint64_t>(t0 < k1 ? t0 : k0) * ldx2;
   };
+  // this wave's DMAs of stage p (p < NB) before the loop
+  auto first_dmas = [&](int p, int32_t idxv) {
+    const int64_t t0 = twave + p * KB;
+    const int rem = stage_rem(t0);
+    const char* base = stage_base(t0);
+#pragma unroll
+    for (int i = 0; i < kDmaWave; ++i) dma_i(i, lds_u32 + p * kStageB + wave_dst, rem, idxv, base);
+  };
 
-  if (n_stages > 0) {
-    bf16x8_t fa[2][4], fb[2][2];
+  // The K loop of one wave: NM MFMAs per K-step into acc[NM], fragments at
+  // the NR LDS offsets off[] (read order).
+  auto run = [&](auto& acc, const auto& off) __attribute__((always_inline)) {
+    constexpr int NM = static_cast<int>(sizeof(acc) / sizeof(acc[0]));
+    constexpr int NR = static_cast<int>(sizeof(off) / sizeof(off[0]));
 #pragma unroll
-    for (int p = 0; p < NB - 1; ++p) {
-      const int64_t t0 = twave + p * KB;
-      const int32_t idx0 = load_idx(t0);
-      const int rem = stage_rem(t0);
-      const char* base = stage_base(t0);
+    for (int j = 0; j < NM; ++j)
 #pragma unroll
-      for (int i = 0; i < kDmaWave; ++i) dma_i(i, lds_u32 + p * kStageB + wave_dst, rem, idx0, base);
-    }
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    if (n_stages <= 0) return;
+    bf16x8_t fr[2][NR];
+#pragma unroll
+    for (int p = 0; p < NB - 1; ++p) first_dmas(p, load_idx(twave + p * KB));
     int32_t idx_n = load_idx(twave + (NB - 1) * KB);
     __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int qq = 0; qq < 6; ++qq) SYRK_READ(0, qq, 0u);
-    {
-      const int64_t t0 = twave + (NB - 1) * KB;
-      const int rem = stage_rem(t0);
-      const char* base = stage_base(t0);
-#pragma unroll
-      for (int i = 0; i < kDmaWave; ++i)
-        dma_i(i, lds_u32 + (NB - 1) * kStageB + wave_dst, rem, idx_n, base);
-    }
+    for (int qq = 0; qq < NR; ++qq) SYRK_READ(0, qq, 0u);
+    first_dmas(NB - 1, idx_n);
     __builtin_amdgcn_sched_barrier(0);
     int rbuf = 0;
     for (int s = 0; s < n_stages - 1; ++s) {
@@ -356,9 +387,9 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int ks = 1; ks < nks; ++ks) {
         const int P = (ks - 1) & 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < NM; ++j) {
           SYRK_MFMA(P, j);
-          if (j < 6) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
+          if (j < NR) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
           if (GATHER && ks == 1 && j == 1)
             idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
           __builtin_amdgcn_sched_barrier(0);
@@ -376,10 +407,10 @@ __global__ void __launch_bounds__(kThreads, 1)
       const char* base = stage_base(t0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < NM; ++j) {
         SYRK_MFMA(L, j);
-        if (j < 6) SYRK_READ(L ^ 1, j, nrd);
-        if (j % kDmaEvery == kDmaEvery - 1) dma_i(j / kDmaEvery, dst, rem, idx_n, base);
+        if (j < NR) SYRK_READ(L ^ 1, j, nrd);
+        if (j < 8 && j % kDmaEvery == kDmaEvery - 1) dma_i(j / kDmaEvery, dst, rem, idx_n, base);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -389,21 +420,93 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int ks = 1; ks < nks; ++ks) {
         const int P = (ks - 1) & 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < NM; ++j) {
           SYRK_MFMA(P, j);
-          if (j < 6) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
+          if (j < NR) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) SYRK_MFMA(L, j);
+      for (int j = 0; j < NM; ++j) SYRK_MFMA(L, j);
     }
     __builtin_amdgcn_s_waitcnt(0);
+  };
+
+  if (dtile) {
+    const int h = wave >> 2;
+    const int rho = ((wave & 3) + 2 * h) & 3;  // 0, 1: a 4x2 part; 2, 3: a triangle
+    const uint32_t tile = static_cast<uint32_t>(h ? it.tj : it.ti) * kTile;
+    if (h == 1 && diag) {
+      // a single diagonal tile: the B half repeats the A half; DMAs only
+      if (n_stages > 0) {
+#pragma unroll
+        for (int p = 0; p < NB - 1; ++p) first_dmas(p, load_idx(twave + p * KB));
+        int32_t idx_n = load_idx(twave + (NB - 1) * KB);
+        __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+        __builtin_amdgcn_s_barrier();
+        first_dmas(NB - 1, idx_n);
+        int rbuf = 0;
+        for (int s = 0; s < n_stages - 1; ++s) {
+          idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
+          const uint32_t wbuf = static_cast<uint32_t>(rbuf);
+          rbuf = rbuf + 1 == NB ? 0 : rbuf + 1;
+          __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+          __builtin_amdgcn_s_barrier();
+          const int64_t t0 = twave + static_cast<int64_t>(s + NB) * KB;
+          const int rem = stage_rem(t0);
+          const char* base = stage_base(t0);
+#pragma unroll
+          for (int i = 0; i < kDmaWave; ++i)
+            dma_i(i, lds_u32 + wbuf * kStageB + wave_dst, rem, idx_n, base);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      return;
+    }
+    if (rho >= 2) {
+      const int m0 = 4 * (rho - 2);
+      const uint32_t off[4] = {frag_off(h, m0), frag_off(h, m0 + 1), frag_off(h, m0 + 2),
+                               frag_off(h, m0 + 3)};
+      f32x16_t acc[10];
+      run(acc, off);
+      flush_tri(acc, out, ld, accumulate != 0, static_cast<uint32_t>(C),
+                tile + 128 * static_cast<uint32_t>(rho - 2), lane);
+      return;
+    }
   }
-  const bool interior =
-      direct && it.ti > it.tj && (static_cast<int64_t>(it.ti) + 1) * kTile <= C;
-  flush<2>(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
-           interior);
+  // a 4x2 part: rows 128 wr.., columns 64 wc.. of an off-diagonal (or split)
+  // tile, or rows 128.., columns 64 rho.. of a diagonal tile
+  uint32_t off[6], gi0, gj0;
+  bool interior;
+  if (dtile) {
+    const int h = wave >> 2;
+    const int rho = ((wave & 3) + 2 * h) & 3;
+    const uint32_t tile = static_cast<uint32_t>(h ? it.tj : it.ti) * kTile;
+    off[0] = frag_off(h, 4);
+    off[1] = frag_off(h, 2 * rho);
+    off[2] = frag_off(h, 2 * rho + 1);
+    off[3] = frag_off(h, 5);
+    off[4] = frag_off(h, 6);
+    off[5] = frag_off(h, 7);
+    gi0 = tile + 128;
+    gj0 = tile + 64 * static_cast<uint32_t>(rho);
+    interior = static_cast<int64_t>(tile) + kTile <= C;
+  } else {
+    const int wr = wave >> 2, wc = wave & 3;
+    off[0] = frag_off(0, 4 * wr);
+    off[1] = frag_off(1, 2 * wc);
+    off[2] = frag_off(1, 2 * wc + 1);
+    off[3] = frag_off(0, 4 * wr + 1);
+    off[4] = frag_off(0, 4 * wr + 2);
+    off[5] = frag_off(0, 4 * wr + 3);
+    gi0 = (direct ? static_cast<uint32_t>(it.ti) * kTile : 0u) + wr * 128;
+    gj0 = (direct ? static_cast<uint32_t>(it.tj) * kTile : 0u) + wc * 64;
+    interior = direct && it.ti > it.tj && (static_cast<int64_t>(it.ti) + 1) * kTile <= C;
+  }
+  f32x16_t acc[8];
+  run(acc, off);
+  flush_part(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
+             interior);
 }
 #undef SYRK_MFMA
 #undef SYRK_READ
@@ -524,10 +627,32 @@ std::vector<std::pair<int32_t, int32_t>> blocked_tiles(int64_t nt) {
   return t;
 }
 
+// Direct items pair a group's diagonal tiles in the order above: (d, d')
+// with d < d' stands for tiles (d, d) and (d', d') (see syrk_kernel); an odd
+// one out stays (d, d).
+std::vector<std::pair<int32_t, int32_t>> pair_diagonals(
+    const std::vector<std::pair<int32_t, int32_t>>& tiles) {
+  std::vector<std::pair<int32_t, int32_t>> out;
+  int64_t open = -1;  // index in out of an unpaired diagonal tile
+  for (const auto& t : tiles) {
+    if (t.first != t.second) {
+      out.push_back(t);
+    } else if (open >= 0) {
+      out[open].second = t.first;
+      open = -1;
+    } else {
+      open = static_cast<int64_t>(out.size());
+      out.push_back(t);
+    }
+  }
+  return out;
+}
+
 int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t target_items,
                Plan* plan) {
   const int64_t nt = ceil_div(C, kTile);
   const auto tiles = blocked_tiles(nt);
+  const auto dtiles = pair_diagonals(tiles);
   const int64_t T = static_cast<int64_t>(tiles.size());
   int64_t active = 0, n_max = 0, total_tokens = 0;
   for (int64_t g = 0; g < n_groups; ++g) {
@@ -584,7 +709,7 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
     std::vector<HessItem> gi;
     gi.reserve(T * S);
     if (S == 1) {
-      for (const auto& t : tiles)
+      for (const auto& t : dtiles)
         gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second, -1, k0, k1});
     } else {
       const int64_t slot_base = n_slots;
