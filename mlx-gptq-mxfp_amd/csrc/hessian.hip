@@ -605,9 +605,11 @@ __global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __re
 //     launch has few tile items (one dense layer), the token range is split
 //     further to fill the 256 CUs, choosing the split count by a cost model
 //     (rounds of 256 items x tokens per item, plus the partial-tile traffic).
-//     Partial tiles are summed in a fixed order by reduce_split_kernel, so H
-//     is deterministic. target_items > 0 instead sets the split directly
-//     (chunk = max(2048, tokens*tiles/target_items)).
+//     In a launch of several groups, a group longer than the average per-CU
+//     load is split too. Partial tiles are summed in a fixed order by
+//     reduce_split_kernel, so H is deterministic. target_items > 0 instead
+//     sets the split directly (chunk = max(2048, tokens*tiles/target_items));
+//   - direct (unsplit) items pair a group's diagonal tiles.
 // ---------------------------------------------------------------------------
 struct Plan {
   PlanHeader hdr;
@@ -686,6 +688,17 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
     }
   }
 
+  // Multi-group launches: a group whose items would each run longer than the
+  // average per-CU load (tokens x items / CUs) is split along K, so that its
+  // few long items do not keep one XCD busy after the others finish (a routed
+  // down projection with C = 768 has 5 items per expert, and its heaviest
+  // expert can hold 1.4x the average CU load).
+  int64_t heavy_cap = 0;
+  if (chunk_explicit == 0 && n_groups > 1) {
+    const int64_t avg = total_tokens * static_cast<int64_t>(dtiles.size()) / kCUs;
+    heavy_cap = std::max<int64_t>(avg, 4096);
+  }
+
   struct Chunk {
     int64_t work;
     std::vector<HessItem> items;
@@ -701,7 +714,8 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
     } else if (chunk_explicit > 0) {
       per = std::min<int64_t>(chunk_explicit, kMaxItemTokens);
     } else {
-      const int64_t S = std::max<int64_t>(ceil_div(n, kMaxItemTokens), s_bal);
+      int64_t S = std::max<int64_t>(ceil_div(n, kMaxItemTokens), s_bal);
+      if (heavy_cap > 0 && n > heavy_cap) S = std::max<int64_t>(S, ceil_div(n, heavy_cap));
       per = ceil_div(n, S);
     }
     per = ceil_div(per, kKs) * kKs;

@@ -88,6 +88,38 @@ def test_gathered_hessian_wide_addressing(monkeypatch):
             assert hessian_ref.rel_frobenius(H64[gi].cpu(), hessian_ref.hessian_fp64(rows)) < TOL
 
 
+@pytest.mark.parametrize("C", [768, 1000])
+def test_heavy_groups_split_and_diagonal_pairs(C):
+    """A multi-group gathered launch in which the heaviest groups are split
+    along K (partial tiles, summed by the reduce kernel) while the others run
+    whole with their diagonal tiles in pairs (C = 768: one pair and one odd
+    tile; C = 1000: two pairs, the last tile ragged). Every group against
+    float64, exact symmetry, and accumulation onto the first result."""
+    from mlx_gptq import capture
+
+    N = 12000
+    X = _rows(N, C, seed=C)
+    g = torch.Generator().manual_seed(C + 1)
+    sizes = [300, 9000, 0, 5000, 120]
+    idx = torch.cat([torch.randint(0, N, (s,), generator=g) for s in sizes]).to(torch.int32)
+    off = [0]
+    for s in sizes:
+        off.append(off[-1] + s)
+    Xd, idd = X.to(DEV), idx.to(DEV)
+    H = capture.grouped_hessian(Xd, off, row_index=idd)
+    Hc = H.cpu()
+    for gi, s in enumerate(sizes):
+        if s == 0:
+            assert torch.count_nonzero(Hc[gi]) == 0
+            continue
+        rows = X[idx[off[gi] : off[gi + 1]].long()]
+        assert hessian_ref.rel_frobenius(Hc[gi], hessian_ref.hessian_fp64(rows)) < TOL
+        assert torch.equal(Hc[gi], Hc[gi].T)
+    out = H.clone()
+    capture.grouped_hessian(Xd, off, row_index=idd, out=out, accumulate=True)
+    assert torch.equal(out.cpu(), 2 * Hc)  # the same launch again, added exactly
+
+
 def test_split_k_partials_and_accumulate():
     from mlx_gptq import capture
 
