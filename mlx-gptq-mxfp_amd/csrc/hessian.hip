@@ -200,16 +200,17 @@ __device__ inline void flush_tri(f32x16_t (&acc)[10], float* __restrict__ out, u
 // transposed read takes from each of its 8 token rows land on four distinct
 // 64-byte bank groups (no conflicts).
 //
-// Schedule of one stage s (nks = KB/16 K-steps of 8 MFMAs, the 4x2 blocks
-// of the wave's 128x64 part): segment k (k = 1..nks-1) runs the 8 MFMAs of
-// K-step k-1, the first six each followed by one of the six fragment reads
-// (a0 b0 b1 a1 a2 a3) of K-step k. Then the stage barrier (this wave's DMA
+// Schedule of one stage s (nks = KB/16 K-steps of 8 MFMAs for the 4x2
+// blocks of a 128x64 part, 10 for a triangle): segment k (k = 1..nks-1) runs
+// the MFMAs of K-step k-1, the first ones each followed by one of the
+// fragment reads of K-step k (six for a 4x2 part, a0 b0 b1 a1 a2 a3; four
+// for a triangle). Then the stage barrier (this wave's DMA
 // of stage s+1 done: vmcnt; every wave done reading stage s: lgkmcnt(0)
 // before s_barrier), after which segment 0 of stage s+1 runs the last
 // K-step's MFMAs of stage s together with the first fragment reads of stage
 // s+1 and the DMA of stage s+NB into the buffer stage s just released.
-// Fragments are double-buffered in VGPRs (fa[2][4], fb[2][2]); each MFMA is
-// fenced by sched_barrier so this order is kept.
+// Fragments are double-buffered in VGPRs (fr[2][6] or fr[2][4]); each MFMA
+// is fenced by sched_barrier so this order is kept.
 __device__ inline void dma_tok(uint32_t lds_dst, uint32_t voffset, const char* saddr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
