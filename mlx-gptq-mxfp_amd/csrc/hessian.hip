@@ -56,7 +56,7 @@ struct HessItem {
 };
 
 struct SplitTile {
-  int32_t g, ti, tj, slot0, nslots, pad;
+  int32_t g, ti, tj, slot0, nslots, stride;  // slots slot0 + stride * i, i < nslots
 };
 
 struct PlanHeader {
@@ -161,18 +161,21 @@ __device__ inline void flush_part(f32x16_t (&acc)[8], float* __restrict__ out, u
 }
 
 // Flush the lower triangle of a 128x128 diagonal part at rows and columns
-// base.. of H (direct only): its strictly-lower blocks inside H are stored
-// whole and mirrored, its diagonal blocks (and blocks crossing C) masked.
+// base.. of `out`: into H (direct), its strictly-lower blocks inside H
+// stored whole and mirrored, its diagonal blocks (and blocks crossing C)
+// masked; into a partial tile's slot, every block as it is (the blocks above
+// the diagonal are never written, and the reduction reads only the lower
+// triangle of a diagonal tile).
 __device__ inline void flush_tri(f32x16_t (&acc)[10], float* __restrict__ out, uint32_t ld_s,
-                                 bool add, uint32_t C, uint32_t base, int lane) {
+                                 bool direct, bool add, uint32_t C, uint32_t base, int lane) {
   const uint32_t ld = ld_vgpr(ld_s);
   const uint32_t gj_l = base + (lane & 31);
   const uint32_t gi_l = base + 4 * (lane >> 5);
 #pragma unroll
   for (int j = 0; j < 10; ++j) {
     const int r = tri_row(j), c = tri_col(j);
-    const bool whole = c < r && base + 32 * r + 32 <= C;
-    flush_block(acc[j], out, ld, whole, true, add, C, gi_l + 32 * r, gj_l + 32 * c);
+    const bool whole = direct && c < r && base + 32 * r + 32 <= C;
+    flush_block(acc[j], out, ld, whole, direct, add, C, gi_l + 32 * r, gj_l + 32 * c);
   }
 }
 
@@ -239,7 +242,7 @@ __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
 // wave's MFMAs; with one wave per SIMD (a 128x128 quarter each) the same
 // stall idled the pipe (measured 3-6 % slower, same results bit for bit).
 //
-// Diagonal tiles of direct launches. An item with ti <= tj is diagonal:
+// Diagonal tiles. An item with ti <= tj is diagonal:
 // ti == tj one tile, ti < tj the pair of tiles (ti, ti) and (tj, tj), whose
 // channels the A and B halves of the LDS rows hold (a pair moves the same
 // 1 KB per token as an off-diagonal tile). Each diagonal tile is cut into
@@ -250,7 +253,8 @@ __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
 // arranged so that each SIMD runs one 4x2 part and one triangle: 18 MFMAs per
 // K-step against 16 for an off-diagonal tile, for two tiles. A single
 // diagonal tile leaves waves 4-7 with their DMAs only (10 MFMAs per K-step on
-// the busiest SIMD).
+// the busiest SIMD). A pair's partial tiles (split items) go to slots slot
+// and slot + 1.
 #define SYRK_MFMA(P, j)                                                                   \
   acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[P][op_a<NM>(j)], fr[P][op_b<NM>(j)], \
                                                    acc[j], 0, 0, 0)
@@ -282,7 +286,7 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool diag = it.ti == it.tj;
   const bool direct = it.slot < 0;
-  const bool dtile = direct && it.ti <= it.tj;  // one diagonal tile or a pair
+  const bool dtile = it.ti <= it.tj;  // one diagonal tile or a pair
   float* out = direct ? H + static_cast<int64_t>(it.g) * C * C
                       : partials + static_cast<int64_t>(it.slot) * kTile * kTile;
   const uint32_t ld = direct ? static_cast<uint32_t>(C) : kTile;
@@ -436,7 +440,8 @@ __global__ void __launch_bounds__(kThreads, 1)
   if (dtile) {
     const int h = wave >> 2;
     const int rho = ((wave & 3) + 2 * h) & 3;  // 0, 1: a 4x2 part; 2, 3: a triangle
-    const uint32_t tile = static_cast<uint32_t>(h ? it.tj : it.ti) * kTile;
+    const uint32_t tile = direct ? static_cast<uint32_t>(h ? it.tj : it.ti) * kTile : 0u;
+    float* out_h = out + (!direct && h ? kTile * kTile : 0);
     if (h == 1 && diag) {
       // a single diagonal tile: the B half repeats the A half; DMAs only
       if (n_stages > 0) {
@@ -470,7 +475,7 @@ __global__ void __launch_bounds__(kThreads, 1)
                                frag_off(h, m0 + 3)};
       f32x16_t acc[10];
       run(acc, off);
-      flush_tri(acc, out, ld, accumulate != 0, static_cast<uint32_t>(C),
+      flush_tri(acc, out_h, ld, direct, direct && accumulate, static_cast<uint32_t>(C),
                 tile + 128 * static_cast<uint32_t>(rho - 2), lane);
       return;
     }
@@ -479,10 +484,12 @@ __global__ void __launch_bounds__(kThreads, 1)
   // tile, or rows 128.., columns 64 rho.. of a diagonal tile
   uint32_t off[6], gi0, gj0;
   bool interior;
+  float* out_p = out;
   if (dtile) {
     const int h = wave >> 2;
     const int rho = ((wave & 3) + 2 * h) & 3;
-    const uint32_t tile = static_cast<uint32_t>(h ? it.tj : it.ti) * kTile;
+    const uint32_t tile = direct ? static_cast<uint32_t>(h ? it.tj : it.ti) * kTile : 0u;
+    out_p = out + (!direct && h ? kTile * kTile : 0);
     off[0] = frag_off(h, 4);
     off[1] = frag_off(h, 2 * rho);
     off[2] = frag_off(h, 2 * rho + 1);
@@ -491,7 +498,7 @@ __global__ void __launch_bounds__(kThreads, 1)
     off[5] = frag_off(h, 7);
     gi0 = tile + 128;
     gj0 = tile + 64 * static_cast<uint32_t>(rho);
-    interior = static_cast<int64_t>(tile) + kTile <= C;
+    interior = direct && static_cast<int64_t>(tile) + kTile <= C;
   } else {
     const int wr = wave >> 2, wc = wave & 3;
     off[0] = frag_off(0, 4 * wr);
@@ -506,8 +513,8 @@ __global__ void __launch_bounds__(kThreads, 1)
   }
   f32x16_t acc[8];
   run(acc, off);
-  flush_part(acc, out, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0, lane,
-             interior);
+  flush_part(acc, out_p, ld, direct, direct && accumulate, static_cast<uint32_t>(C), gi0, gj0,
+             lane, interior);
 }
 #undef SYRK_MFMA
 #undef SYRK_READ
@@ -549,7 +556,8 @@ __global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __re
       float4 t[kRedSlots];
 #pragma unroll
       for (int i = 0; i < kRedSlots; ++i)
-        if (s0 + i < st.nslots) t[i] = *reinterpret_cast<const float4*>(p0 + (s0 + i) * kSlot + e);
+        if (s0 + i < st.nslots)
+          t[i] = *reinterpret_cast<const float4*>(p0 + static_cast<int64_t>(s0 + i) * st.stride * kSlot + e);
 #pragma unroll
       for (int i = 0; i < kRedSlots; ++i)
         if (s0 + i < st.nslots) {
@@ -602,15 +610,16 @@ __global__ void __launch_bounds__(256) reduce_split_kernel(const SplitTile* __re
 //   - a group's item list is cut into at most 8 contiguous runs (>= 32 items)
 //     that go to the least-loaded XCD, heaviest first (LPT), and the XCD
 //     queues are interleaved into the grid;
-//   - K splits: every item covers at most kMaxItemTokens tokens; when the
-//     launch has few tile items (one dense layer), the token range is split
-//     further to fill the 256 CUs, choosing the split count by a cost model
-//     (rounds of 256 items x tokens per item, plus the partial-tile traffic).
-//     In a launch of several groups, a group longer than the average per-CU
-//     load is split too. Partial tiles are summed in a fixed order by
+//   - K splits: every item covers at most kMaxItemTokens tokens; when a
+//     one-group launch has few tile items (one dense layer), the token range
+//     is split further to fill the 256 CUs, choosing the split count by a
+//     cost model (rounds of 256 items x tokens per item, plus the
+//     partial-tile traffic). In a launch of several groups, a group longer
+//     than the average per-CU load is split instead. Partial tiles are summed in a fixed order by
 //     reduce_split_kernel, so H is deterministic. target_items > 0 instead
 //     sets the split directly (chunk = max(2048, tokens*tiles/target_items));
-//   - direct (unsplit) items pair a group's diagonal tiles.
+//   - items pair a group's diagonal tiles (a split pair's two partial tiles
+//     take interleaved slots).
 // ---------------------------------------------------------------------------
 struct Plan {
   PlanHeader hdr;
@@ -630,7 +639,7 @@ std::vector<std::pair<int32_t, int32_t>> blocked_tiles(int64_t nt) {
   return t;
 }
 
-// Direct items pair a group's diagonal tiles in the order above: (d, d')
+// Items pair a group's diagonal tiles in the order above: (d, d')
 // with d < d' stands for tiles (d, d) and (d', d') (see syrk_kernel); an odd
 // one out stays (d, d).
 std::vector<std::pair<int32_t, int32_t>> pair_diagonals(
@@ -654,8 +663,7 @@ std::vector<std::pair<int32_t, int32_t>> pair_diagonals(
 int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t target_items,
                Plan* plan) {
   const int64_t nt = ceil_div(C, kTile);
-  const auto tiles = blocked_tiles(nt);
-  const auto dtiles = pair_diagonals(tiles);
+  const auto tiles = pair_diagonals(blocked_tiles(nt));
   const int64_t T = static_cast<int64_t>(tiles.size());
   int64_t active = 0, n_max = 0, total_tokens = 0;
   for (int64_t g = 0; g < n_groups; ++g) {
@@ -671,7 +679,10 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
   if (target_items > 0) {
     const int64_t work = std::max<int64_t>(total_tokens, 1) * T;
     chunk_explicit = std::max<int64_t>(2048, ceil_div(work, target_items));
-  } else {
+  } else if (active == 1) {
+    // one group (a dense layer): split to fill the CUs. Launches of several
+    // groups split only their heavy groups (below): this model prices every
+    // item at the longest group's tokens, which misjudges skewed groups.
     const int64_t base = active * T;
     if (base > 0 && base < 8 * kCUs) {
       double best = 1e300;
@@ -696,7 +707,7 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
   // expert can hold 1.4x the average CU load).
   int64_t heavy_cap = 0;
   if (chunk_explicit == 0 && n_groups > 1) {
-    const int64_t avg = total_tokens * static_cast<int64_t>(dtiles.size()) / kCUs;
+    const int64_t avg = total_tokens * T / kCUs;
     heavy_cap = std::max<int64_t>(avg, 4096);
   }
 
@@ -724,23 +735,35 @@ int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t targ
     std::vector<HessItem> gi;
     gi.reserve(T * S);
     if (S == 1) {
-      for (const auto& t : dtiles)
+      for (const auto& t : tiles)
         gi.push_back(HessItem{static_cast<int32_t>(g), t.first, t.second, -1, k0, k1});
     } else {
-      const int64_t slot_base = n_slots;
+      // a tile's partials take S slots; a pair's two tiles take 2S, chunk c's
+      // at 2c (tile (ti, ti)) and 2c + 1 (tile (tj, tj))
+      std::vector<int64_t> first(T);
+      for (int64_t e = 0; e < T; ++e) {
+        first[e] = n_slots;
+        n_slots += (tiles[e].first < tiles[e].second ? 2 : 1) * S;
+      }
       for (int64_t c = 0; c < S; ++c) {
         const int64_t a = k0 + c * per;
-        for (int64_t ti = 0; ti < T; ++ti)
-          gi.push_back(HessItem{static_cast<int32_t>(g), tiles[ti].first, tiles[ti].second,
-                                static_cast<int32_t>(slot_base + ti * S + c), a,
+        for (int64_t e = 0; e < T; ++e) {
+          const bool pair = tiles[e].first < tiles[e].second;
+          gi.push_back(HessItem{static_cast<int32_t>(g), tiles[e].first, tiles[e].second,
+                                static_cast<int32_t>(first[e] + (pair ? 2 * c : c)), a,
                                 std::min(a + per, k1)});
+        }
       }
-      for (int64_t ti = 0; ti < T; ++ti)
-        plan->split.push_back(SplitTile{static_cast<int32_t>(g), tiles[ti].first,
-                                        tiles[ti].second,
-                                        static_cast<int32_t>(slot_base + ti * S),
-                                        static_cast<int32_t>(S), 0});
-      n_slots += T * S;
+      for (int64_t e = 0; e < T; ++e) {
+        const int32_t ti = tiles[e].first, tj = tiles[e].second;
+        const int32_t f = static_cast<int32_t>(first[e]), ns = static_cast<int32_t>(S);
+        if (ti < tj) {
+          plan->split.push_back(SplitTile{static_cast<int32_t>(g), ti, ti, f, ns, 2});
+          plan->split.push_back(SplitTile{static_cast<int32_t>(g), tj, tj, f + 1, ns, 2});
+        } else {
+          plan->split.push_back(SplitTile{static_cast<int32_t>(g), ti, tj, f, ns, 1});
+        }
+      }
     }
     const int64_t n_items = static_cast<int64_t>(gi.size());
     const int64_t parts = std::min<int64_t>(kXcds, std::max<int64_t>(1, n_items / 32));
