@@ -480,8 +480,9 @@ __global__ void __launch_bounds__(kThreads, 1)
       return;
     }
   }
-  // a 4x2 part: rows 128 wr.., columns 64 wc.. of an off-diagonal (or split)
-  // tile, or rows 128.., columns 64 rho.. of a diagonal tile
+  // a 4x2 part: rows 128 wr.., columns 64 wc.. of an off-diagonal tile (into
+  // H, or its partial slot), or rows 128.., columns 64 rho.. of a diagonal
+  // tile
   uint32_t off[6], gi0, gj0;
   bool interior;
   float* out_p = out;
