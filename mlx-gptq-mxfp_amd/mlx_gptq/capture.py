@@ -128,7 +128,9 @@ def grouped_hessian(
 ) -> torch.Tensor:
     """H[g] (+)= X_g^T X_g for every group g, fp32 [G, C, C].
 
-    X: bf16 [N, C] on a HIP device (row-contiguous). Group g uses the token
+    X: bf16 [N, C] on a HIP device (row-contiguous; any C, a C that is not a
+    multiple of 8 or rows that are not 16-byte aligned go through a padded
+    copy). Group g uses the token
     list entries offsets[g]:offsets[g+1]; entry t selects row
     ``row_index[t]`` of X (or row t when ``row_index`` is None).
     ``validate`` checks the gather indices first (one device reduction and a
@@ -154,11 +156,27 @@ def grouped_hessian(
                 raise IndexError(f"row_index outside [0, {X.shape[0]})")
     elif int(off[-1]) > X.shape[0]:
         raise ValueError("offsets exceed the rows of X")
+    if out is not None and (out.shape != (G, C, C) or out.dtype != torch.float32
+                            or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous float32 [{G}, {C}, {C}] tensor")
+    if C % 8 or X.stride(0) % 8 or X.data_ptr() % 16:
+        # The kernel moves rows in 16-byte pieces. Zero columns add nothing
+        # to X^T X, so such X is solved as a zero-padded copy and H is the
+        # padded result's leading C x C block.
+        C8 = -(-C // 8) * 8
+        Xp = torch.zeros(X.shape[0], C8, dtype=torch.bfloat16, device=dev)
+        Xp[:, :C] = X
+        Hp = grouped_hessian(Xp, off, row_index, None, False, target_items, validate=False)
+        if out is None:
+            return Hp[:, :C, :C].contiguous()
+        if accumulate:
+            out += Hp[:, :C, :C]
+        else:
+            out.copy_(Hp[:, :C, :C])
+        return out
     if out is None:
         out = torch.empty(G, C, C, dtype=torch.float32, device=dev)
         accumulate = False
-    elif out.shape != (G, C, C) or out.dtype != torch.float32 or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous float32 [{G}, {C}, {C}] tensor")
     stream = nat.stream_of(dev)
     plan, ws = _hessian_plan(dev, stream, C, off, target_items)
     nat.call(

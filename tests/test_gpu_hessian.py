@@ -88,6 +88,37 @@ def test_gathered_hessian_wide_addressing(monkeypatch):
             assert hessian_ref.rel_frobenius(H64[gi].cpu(), hessian_ref.hessian_fp64(rows)) < TOL
 
 
+@pytest.mark.parametrize("c", [1, 13, 100, 2051])
+def test_channel_counts_not_multiple_of_8(c):
+    """Any C (the reference's Stash.hessian takes any width): dense, grouped
+    and gathered, and accumulation into a caller's H, against float64; also
+    rows that are not 16-byte aligned (a column slice of a wider matrix)."""
+    from mlx_gptq import capture
+
+    N = 3000
+    X = _rows(N, c, seed=c)
+    H = capture.hessian_xtx(X.to(DEV)).cpu()
+    assert H.shape == (c, c) and torch.equal(H, H.T)
+    assert hessian_ref.rel_frobenius(H, hessian_ref.hessian_fp64(X)) < TOL
+    g = torch.Generator().manual_seed(c)
+    sizes = [700, 0, 1800]
+    idx = torch.cat([torch.randint(0, N, (k,), generator=g) for k in sizes]).to(torch.int32)
+    off = [0, 700, 700, 2500]
+    out = torch.zeros(3, c, c, device=DEV)
+    capture.grouped_hessian(X.to(DEV), off, row_index=idx.to(DEV), out=out)
+    capture.grouped_hessian(X.to(DEV), off, row_index=idx.to(DEV), out=out, accumulate=True)
+    Hg = out.cpu()
+    for gi in range(3):
+        rows = X[idx[off[gi] : off[gi + 1]].long()]
+        if rows.shape[0] == 0:
+            assert torch.count_nonzero(Hg[gi]) == 0
+            continue
+        assert hessian_ref.rel_frobenius(Hg[gi], 2 * hessian_ref.hessian_fp64(rows)) < TOL
+    wide = _rows(N, c + 3, seed=c + 1).to(DEV)
+    Hs = capture.hessian_xtx(wide[:, 3:]).cpu()  # rows offset by 6 bytes
+    assert hessian_ref.rel_frobenius(Hs, hessian_ref.hessian_fp64(wide[:, 3:].cpu())) < TOL
+
+
 @pytest.mark.parametrize("C", [768, 1000])
 def test_heavy_groups_split_and_diagonal_pairs(C):
     """A multi-group gathered launch in which the heaviest groups are split
