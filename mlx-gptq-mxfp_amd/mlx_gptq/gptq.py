@@ -153,9 +153,10 @@ def _staged(W: torch.Tensor, H: torch.Tensor, w_dtype: torch.dtype | None = None
         raise RuntimeError(f"W on {W.device} but H on {H.device}")
 
     def put(t, dt):
-        if t.device == dev and t.dtype == dt and t.is_contiguous():
+        # the kernels read 16-byte pieces: a misaligned tensor is staged too
+        if t.device == dev and t.dtype == dt and t.is_contiguous() and t.data_ptr() % 16 == 0:
             return t
-        return t.to(device=dev, dtype=dt).contiguous()
+        return t.to(device=dev, dtype=dt, copy=True).contiguous()
 
     return put(W, w_dtype or W.dtype), put(H, torch.float32)
 

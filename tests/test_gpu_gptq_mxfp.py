@@ -258,6 +258,42 @@ def test_gptq_quantize_in_place_semantics():
         gptq.solve_gptq(Wd[:, :, :48], Hd[:, :48, :48].contiguous(), 4, 32, mode="mxfp4")
 
 
+@pytest.mark.parametrize("mode", ["mxfp4", "affine"])
+def test_unaligned_and_strided_inputs_equal_the_aligned_call(mode):
+    """W and H given as a misaligned contiguous view (storage offset of one
+    element) or as a strided slice solve exactly like aligned copies, through
+    solve_gptq and in place through gptq_quantize (the result lands in the
+    caller's tensor)."""
+    from mlx_gptq import gptq
+
+    W, H, _ = _setup(B=2, R=16, C=64)
+    G = 32 if mode == "mxfp4" else 64
+    kw = dict(mode=mode)
+    ref = gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), 4, G, **kw)
+
+    def misaligned(t):
+        flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=DEV)
+        v = flat[1:].view(t.shape)
+        v.copy_(t.to(DEV))
+        return v
+
+    Wm, Hm = misaligned(W), misaligned(H)
+    assert Wm.is_contiguous() and Wm.data_ptr() % 16 != 0
+    Wwide = torch.zeros(2, 16, 96, device=DEV)
+    Wwide[:, :, 16:80] = W.to(DEV)
+    for Win, Hin in ((Wm, Hm), (Wwide[:, :, 16:80], H.clone().to(DEV))):
+        got = gptq.solve_gptq(Win, Hin, 4, G, **kw)
+        for a, b in zip(got, ref):
+            if a is None:
+                assert b is None
+            else:
+                assert torch.equal(a.cpu(), b.cpu())
+    Wi = misaligned(W)
+    q, s, _, W_ret, _ = gptq.gptq_quantize(Wi, misaligned(H), 4, G, **kw)
+    assert W_ret.data_ptr() == Wi.data_ptr()
+    assert torch.equal(Wi.cpu(), ref[3].cpu()) and torch.equal(q.cpu(), ref[0].cpu())
+
+
 def test_solver_failure_matches_reference_and_in_place_leaves_w(caplog):
     """A Hessian block that never factors: solve_gptq raises the reference's
     RuntimeError after its warnings (gptq.py:37-63, via the dead-column fix
