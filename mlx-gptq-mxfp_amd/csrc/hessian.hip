@@ -321,6 +321,49 @@ __global__ void __launch_bounds__(kThreads, 1)
 #pragma unroll
   for (int i = 0; i < kDmaWave; ++i) vofs[i] = voff[i & 3] + i * ldx2;
 
+  // L2 prefetch (gathered launches, X < 4 GB): while the DMAs of stage s + NB
+  // are issued, one 2-byte load per 128-byte line brings the rows of stage
+  // s + NB + 1 into the XCD's L2, so that those DMAs find their lines there
+  // instead of missing. The items of one token chunk of a group run
+  // together on one XCD and read the same rows; the lines of each 256-column
+  // block of a stage (KB tokens x 4 lines) are cut into nt slices, and item
+  // (ti, tj) takes slice tj of block ti and slice ti of block tj (a diagonal
+  // item slice d of its block d), so every line is requested once per
+  // token chunk. The loaded values are dead; they are kept live until the
+  // stage barrier's vmcnt(0) so that their registers are not reused while a
+  // load is in flight.
+  constexpr bool kPf = GATHER && !BIG;
+  constexpr int kPfAhead = 1;
+  const int nt = static_cast<int>((C + kTile - 1) / kTile);
+  const int pf_parts = it.ti == it.tj ? 1 : 2;
+  const int pf_S = (4 * KB + nt - 1) / nt;
+  const bool pf_wave = kPf && wave * 64 < pf_parts * pf_S;
+  int pf_tok = 0;
+  uint32_t pf_col = 0;
+  bool pf_ok = false;
+  if (kPf) {
+    const int pi = wave * 64 + lane;
+    const int part = pi / pf_S, r = pi % pf_S;
+    const int b = part == 0 ? it.ti : it.tj;
+    const int o = it.ti > it.tj ? (part == 0 ? it.tj : it.ti) : b;
+    const int Lx = o * pf_S + r;
+    const int col = b * kTile + (Lx & 3) * 64;
+    pf_ok = part < pf_parts && Lx < 4 * KB && col < C;
+    pf_tok = Lx >> 2;
+    pf_col = static_cast<uint32_t>(2 * col);
+  }
+  auto pf_index = [&](int s) -> int32_t {
+    const int64_t t = k0 + static_cast<int64_t>(s + NB + kPfAhead) * KB + pf_tok;
+    return row_index[t < k1 ? t : k1 - 1];
+  };
+  auto pf_load = [&](int s, int32_t pidx) -> uint32_t {
+    const int64_t t = k0 + static_cast<int64_t>(s + NB + kPfAhead) * KB + pf_tok;
+    uint32_t r = static_cast<uint32_t>(pidx);
+    r = r < nr1 ? r : nr1;
+    const uint32_t o = (pf_ok && t < k1) ? r * ldx2 + pf_col : 0u;
+    return X[o >> 1];
+  };
+
   auto load_idx = [&](int64_t t0) -> int32_t {
     if constexpr (GATHER) {
       const int64_t t = t0 + (lane & (kDmaWave - 1));
@@ -386,6 +429,8 @@ __global__ void __launch_bounds__(kThreads, 1)
     first_dmas(NB - 1, idx_n);
     __builtin_amdgcn_sched_barrier(0);
     int rbuf = 0;
+    uint32_t pf_v = 0, pf_sink = 0;
+    int32_t pf_idx = 0;
     for (int s = 0; s < n_stages - 1; ++s) {
       const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
 #pragma unroll
@@ -397,6 +442,7 @@ __global__ void __launch_bounds__(kThreads, 1)
           if (j < NR) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
           if (GATHER && ks == 1 && j == 1)
             idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
+          if (kPf && ks == 1 && j == 2 && pf_wave) pf_idx = pf_index(s);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -416,6 +462,10 @@ __global__ void __launch_bounds__(kThreads, 1)
         SYRK_MFMA(L, j);
         if (j < NR) SYRK_READ(L ^ 1, j, nrd);
         if (j < 8 && j % kDmaEvery == kDmaEvery - 1) dma_i(j / kDmaEvery, dst, rem, idx_n, base);
+        if (kPf && j == NM - 1 && pf_wave) {
+          pf_sink ^= pf_v;
+          pf_v = pf_load(s, pf_idx);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -435,6 +485,7 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int j = 0; j < NM; ++j) SYRK_MFMA(L, j);
     }
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kPf) asm volatile("" ::"v"(pf_sink), "v"(pf_v));
   };
 
   if (dtile) {
