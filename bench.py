@@ -410,9 +410,10 @@ def run_audit(args, torch, np) -> int:
 
 
 def _cpu_setup(torch) -> dict:
-    """CPU leg threads and host description: one
-    thread per core of this process's affinity, capped at the host share the
-    box grants (OMP_NUM_THREADS); the CPU model and the torch build."""
+    """CPU leg threads and host description: one thread per core of this
+    process's affinity (the reference's CPU solve runs multi-threaded
+    torch), capped at the host share the box grants (OMP_NUM_THREADS); the
+    CPU model and the torch build."""
     aff = len(os.sched_getaffinity(0))
     share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or aff
     threads = max(1, min(aff, share))
