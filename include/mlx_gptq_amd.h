@@ -208,7 +208,8 @@ int64_t mgq_gptq_mxfp_workspace_size(int64_t B, int64_t R, int64_t C);
  *   place in H, weights of that column treated as 0), per-group damped
  *   Cholesky-inverse (mgq_prepare_hinv_blocks), fused group solver.
  * W: [B, R, C] of w_dtype (f32 / bf16 / f16), H: f32 [B, C, C] (modified in
- * place as the reference does), C % 32 == 0.
+ * place as the reference does), C % 32 == 0. W, H, W_dq and q_out must be
+ * 16-byte aligned (the kernels move 16-byte pieces; MGQ_ERR_SHAPE otherwise).
  * mode: MGQ_MODE_MXFP4 / MGQ_MODE_MXFP8. algorithm: 0 = groupwise,
  * 1 = safe-scale-search with exponent `offsets[n_offsets]` tried in order
  * (reference: {0,-1,-2,-3,-4,1,2} for mxfp4, {0,-1,1} for mxfp8; <= 8).
