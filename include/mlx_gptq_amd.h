@@ -20,7 +20,9 @@
  *     MGQ_ERR_NOT_PD -> RuntimeError, as the reference raises them.
  *   - Entry points are reentrant: they keep no mutable global state, so one
  *     host thread per device may call them concurrently (the reference's
- *     thread-per-device solve, sequential.py:610-626).
+ *     thread-per-device solve, sequential.py:610-626). The one exception is
+ *     mgq_gptq_mxfp_noalloc, whose calls on one GPU share its scratch array
+ *     (see there).
  *   - Nothing here allocates device memory. Entry points that need scratch
  *     take a caller-owned `workspace` of at least the size reported by the
  *     matching *_workspace_size query.
