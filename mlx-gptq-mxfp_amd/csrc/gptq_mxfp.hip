@@ -65,13 +65,14 @@ __global__ void dead_fix_kernel(float* __restrict__ H, int64_t B, int64_t C,
 
 // Exact reference projection of one element (code and dq), w / scale done
 // as w * inv_scale (identical for power-of-two scales), on the hardware MX
-// conversions.
-template <int MODE>
+// conversions. NONAN: exact only where w * inv_scale is not NaN (the
+// recurrence's fast pass, which a NaN sends to the exact pass anyway).
+template <int MODE, bool NONAN = false>
 __device__ inline uint32_t quant_exact(float w, float inv_scale, float scale, float* dq) {
   if constexpr (MODE == kMxfp4)
-    return mx4_encode_hw(w, inv_scale, scale, dq);
+    return NONAN ? mx4_encode_hw_nonan(w, inv_scale, scale, dq) : mx4_encode_hw(w, inv_scale, scale, dq);
   else
-    return mx8_encode_hw(w, inv_scale, scale, dq);
+    return NONAN ? mx8_encode_hw_nonan(w, inv_scale, scale, dq) : mx8_encode_hw(w, inv_scale, scale, dq);
 }
 
 // (dq - w) / scale of eight weights for scoring a scale candidate.
@@ -520,7 +521,9 @@ __global__ void __launch_bounds__(kThreads)
   // largest. If one fell outside the correction's exact range, or a NaN
   // appeared (it reaches the last error through every later column), the
   // wave runs the recurrence again with div_exact (EXACT = true); a divisor
-  // outside [2^-24, 2^24] (ydiag 0) sends the workgroup there directly.
+  // outside [2^-24, 2^24] (ydiag 0) sends the workgroup there directly. The
+  // fast pass also encodes without the NaN patch (a NaN w_c reaches the last
+  // error as well, so its codes are never kept).
   float errs[kG];
   auto recurrence = [&](auto exact_tag) __attribute__((always_inline)) -> bool {
     constexpr bool EXACT = decltype(exact_tag)::value;
@@ -541,7 +544,7 @@ __global__ void __launch_bounds__(kThreads)
         for (int k = k0; k < c && k < k0 + 4; ++k) acc = acc - errs[k] * u4[k - k0];
       }
       float dq;
-      const uint32_t code = quant_exact<MODE>(acc, inv_scale, scale, &dq);
+      const uint32_t code = quant_exact<MODE, !EXACT>(acc, inv_scale, scale, &dq);
       const float a = acc - dq;  // errs[c] = a / U[c][c]
       if constexpr (EXACT) {
         errs[c] = div_exact(a, col[c], ydiag[c]);

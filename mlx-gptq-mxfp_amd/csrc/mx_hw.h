@@ -93,6 +93,18 @@ __device__ inline uint32_t mx4_encode_hw(float w, float inv_scale, float scale, 
   return code;
 }
 
+// mx4_encode_hw for every w whose n = w * inv_scale is not NaN, without the
+// patch: n + 0 is n, except that -0 becomes +0 (the one non-NaN input whose
+// hardware code, 8, differs from the reference's 0). A NaN n gives an
+// unspecified code; the GPTQ recurrence's fast pass relies on that NaN
+// reaching its last error, which sends the wave to the exact pass.
+__device__ inline uint32_t mx4_encode_hw_nonan(float w, float inv_scale, float scale, float* dq) {
+  const float n = w * inv_scale + 0.0f;
+  const uint32_t code = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, n, 0.0f, 1.0f, 0);
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, 1.0f, 0)[0] * scale;
+  return code;
+}
+
 // Exact E4M3 code of clamp(n, +-448) and dq = value(code) * scale
 // (= e4m3_code_clamped(clamp448(n)), e4m3_value(code) * scale).
 __device__ inline uint32_t mx8_encode_hw(float w, float inv_scale, float scale, float* dq) {
@@ -101,6 +113,17 @@ __device__ inline uint32_t mx8_encode_hw(float w, float inv_scale, float scale, 
   const mx_s16x2_t p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(mx_s16x2_t{0, 0}, c, 0.0f, 1.0f, false);
   uint32_t code = __builtin_bit_cast(uint32_t, p);
   code = (n != n) ? (((f2u(n) >> 24) & 0x80u) | 0x7fu) : code;
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0] * scale;
+  return code;
+}
+
+// mx8_encode_hw for every w whose n = w * inv_scale is not NaN (a NaN n
+// gives an unspecified code, as in mx4_encode_hw_nonan).
+__device__ inline uint32_t mx8_encode_hw_nonan(float w, float inv_scale, float scale, float* dq) {
+  const float n = w * inv_scale;
+  const float c = __builtin_amdgcn_fmed3f(n, -448.0f, 448.0f);
+  const mx_s16x2_t p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(mx_s16x2_t{0, 0}, c, 0.0f, 1.0f, false);
+  const uint32_t code = __builtin_bit_cast(uint32_t, p);
   *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0] * scale;
   return code;
 }
