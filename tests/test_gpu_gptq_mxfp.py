@@ -88,6 +88,34 @@ def test_mxfp_matches_oracle_larger(mode, alg):
     assert torch.all((pl - pl_ref).abs() <= 0.01 * pl_ref.abs()), (pl, pl_ref)
 
 
+@pytest.mark.parametrize("mode,alg", [("mxfp4", "safe-scale-search"), ("mxfp4", "groupwise"),
+                                      ("mxfp8", "groupwise")])
+def test_negative_zero_weights_encode_as_the_reference(mode, alg):
+    """-0 weights (grid.py:82-105: the E2M1 sign bit is set for x < 0 only, so
+    -0 takes code 0 where the hardware conversion gives the sign-only code 8;
+    E4M3 keeps torch's 0x80). The first column of a group sees its weight
+    unchanged, and a group of -0 weights stays zero through the recurrence;
+    both must carry the oracle's codes."""
+    from mlx_gptq import grid, gptq
+
+    W, H, _ = _setup(B=2, R=64, C=256, N=2048, seed=11, scale=0.02)
+    W[:, :, ::32] = -0.0        # the first column of every group
+    W[:, ::4, 64:96] = -0.0     # whole groups
+    W[0, 5, 130:140] = -0.0
+    bits = 4 if mode == "mxfp4" else 8
+    q, s, _, W_dq, _ = gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), bits, 32, mode=mode,
+                                       mxfp_algorithm=alg)
+    rq, rs, _, rW, _ = gptq_ref.solve_gptq(W.clone(), H.clone(), bits, 32, mode=mode,
+                                           mxfp_algorithm=alg)
+    q, s, W_dq = q.cpu(), s.cpu(), W_dq.cpu()
+    zero_code = 0 if mode == "mxfp4" else 0x80
+    assert (rq[:, :, ::32] == zero_code).all() and torch.equal(q[:, :, ::32], rq[:, :, ::32])
+    assert torch.equal(q[:, ::4, 64:96], rq[:, ::4, 64:96])
+    assert torch.equal(s[:, ::4, 2], rs[:, ::4, 2])
+    assert _agree(q, rq) >= 0.995
+    assert torch.equal(grid.dequantize_artifact(q, s, None, mode, 32), W_dq)
+
+
 @pytest.mark.parametrize("mode,alg", [("mxfp4", "safe-scale-search"), ("mxfp8", "groupwise")])
 def test_mxfp_nonfinite_weights_leave_other_groups_on_the_oracle(mode, alg):
     """NaN and inf weights stay inside their own (row, 32-column group): the
