@@ -298,6 +298,10 @@ class RoutedStash:
         self.rows = 0  # rows stored
         self._plan = None
         self._hcache: dict[tuple[int, torch.device], torch.Tensor] = {}
+        # per expert: the names of the ExpertRows views over it, and those of
+        # them that were cleared; rows are dropped once every view is
+        self._views: dict[int, set[str]] = {}
+        self._released: dict[int, set[str]] = {}
         self._lock = threading.RLock()
 
     def _append(self, x: torch.Tensor) -> tuple[torch.Tensor, int]:
@@ -465,6 +469,25 @@ class RoutedStash:
             self._plan = None
             self._hcache.clear()
 
+    def attach_view(self, expert: int, name: str):
+        """Register a per-expert view (``ExpertRows``) of expert `expert`."""
+        with self._lock:
+            self._views.setdefault(int(expert), set()).add(name)
+            self._released.get(int(expert), set()).discard(name)
+
+    def release_view(self, expert: int, name: str):
+        """View `name` of expert `expert` was cleared. Separate gate_proj /
+        up_proj parameters share this stash, while the reference keeps one
+        Stash per parameter and expert: the rows are dropped only once every
+        view of the expert has been cleared, so clearing one sibling leaves
+        the other's rows in place."""
+        e = int(expert)
+        with self._lock:
+            rel = self._released.setdefault(e, set())
+            rel.add(name)
+            if rel >= self._views.get(e, set()):
+                self.drop_expert(e)
+
     def clear(self):
         with self._lock:
             self.chunks.clear()
@@ -474,6 +497,7 @@ class RoutedStash:
             self.rows = 0
             self._plan = None
             self._hcache.clear()
+            self._released.clear()
 
 
 class ExpertCapture:
@@ -728,19 +752,30 @@ class ExpertRows:
         self.expert = int(expert)
         self.name = name
         self.in_features = routed.in_features
+        # set by clear(): the token count kept, as the reference's Stash.clear
+        # keeps .tokens (capture.py:78-79) while its rows are gone
+        self._kept_tokens: int | None = None
+        routed.attach_view(self.expert, name)
 
     @property
     def tokens(self) -> int:
+        if self._kept_tokens is not None:
+            return self._kept_tokens
         return int(self.routed.token_counts()[self.expert])
 
     @property
     def chunks(self) -> list[torch.Tensor]:
         """This expert's rows, gathered into one bf16 [tokens, C] matrix."""
-        if self.tokens == 0:
+        if self._kept_tokens is not None or self.tokens == 0:
             return []
         return [self.routed.expert_rows(self.expert)]
 
     def add(self, x: torch.Tensor):
+        # rows added after a clear make the view live again over the shared
+        # stash (a sibling that was not cleared keeps its earlier rows there)
+        if self._kept_tokens is not None:
+            self._kept_tokens = None
+            self.routed.attach_view(self.expert, self.name)
         self.routed.add_rows(self.expert, x)
 
     def add_sampled(self, x: torch.Tensor, max_rows: int):
@@ -751,15 +786,23 @@ class ExpertRows:
         self.add(rows)
 
     def nbytes(self) -> int:
+        if self._kept_tokens is not None:
+            return 0
         return self.tokens * self.in_features * 2
 
     @torch.no_grad()
     def hessian(self, device, chunk_rows: int = 65536) -> torch.Tensor:
-        """H = X_e^T X_e in fp32 on `device` (capture.py:68-76)."""
-        return self.routed.expert_hessian(self.expert, _hip_device(device))
+        """H = X_e^T X_e in fp32 on `device` (capture.py:68-76); zeros once
+        this view was cleared, as the reference's emptied Stash gives."""
+        dev = _hip_device(device)
+        if self._kept_tokens is not None:
+            return torch.zeros(self.in_features, self.in_features, dtype=torch.float32, device=dev)
+        return self.routed.expert_hessian(self.expert, dev)
 
     def clear(self):
-        self.routed.drop_expert(self.expert)
+        if self._kept_tokens is None:
+            self._kept_tokens = self.tokens
+            self.routed.release_view(self.expert, self.name)
 
 
 class CaptureManager:

@@ -293,12 +293,18 @@ def solve_gptq(
     assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
     # W is a private copy, so the column loop may start before the first
     # damped pass is known to have succeeded; if it had not, solve again from
-    # a fresh copy on the synchronous path (escalation, warnings, errors)
+    # a fresh copy on the synchronous path (escalation, warnings, errors).
+    # The speculative pass has already given H_d's dead columns (diag <= 0)
+    # a unit diagonal, so the retry would no longer see them: their mask is
+    # kept from before, and the retry's copy of W gets those columns zeroed
+    # as the reference's dead-column fix does (gptq.py:216-222).
+    dead = torch.diagonal(H_d, dim1=-2, dim2=-1) <= 0
     W = W0.float().clone()
     res = gptq_affine.gptq_quantize_affine(W, H_d, bits, group_size, damp, clip, storage_dtype,
                                            128, speculative=True)
     if res is None:
         W = W0.float().clone()
+        W.masked_fill_(dead.unsqueeze(1), 0.0)
         res = gptq_quantize(W, H_d, bits, group_size, damp=damp, clip=clip,
                             storage_dtype=storage_dtype, mode=mode, mxfp_algorithm=mxfp_algorithm)
     q, s, b, W_dq, _ = res

@@ -320,6 +320,41 @@ def test_solve_falls_back_when_the_first_damped_pass_fails(caplog):
     assert [r.getMessage() for r in caplog.records] == ref_msgs
 
 
+def test_solve_fallback_keeps_dead_columns_zeroed(caplog):
+    """A batch where one item has dead columns (diag 0 and < 0) and another
+    needs damp 0.1: the speculative first pass fails, and the synchronous
+    retry must still zero the dead columns of its fresh copy of W, as the
+    reference's gptq_quantize does (gptq.py:216-222) before it escalates.
+    Checked against the oracle's solve_gptq on the same inputs."""
+    from mlx_gptq import gptq
+
+    C, R = 128, 48
+    gg = torch.Generator().manual_seed(41)
+    H = torch.zeros(3, C, C)
+    for i in range(3):
+        A = torch.randn(C, C, generator=gg) * 0.01
+        H[i] = A @ A.T + torch.eye(C)
+    H[1, 5, 6] = H[1, 6, 5] = 1.05  # needs damp 0.1 to factor
+    for c, v in ((17, 0.0), (90, -2.0)):  # dead columns of item 0
+        H[0, c, :] = 0.0
+        H[0, :, c] = 0.0
+        H[0, c, c] = v
+    W = torch.randn(3, R, C, generator=gg) * 0.02
+    rq, rs, rb, rW, rrel = gptq_ref.solve_gptq(W.clone(), H.clone(), 4, 64)
+    Hd = H.clone().to(DEV)
+    with caplog.at_level(logging.WARNING, logger="mlx_gptq.gptq"):
+        q, s, b, W_dq, rel = gptq.solve_gptq(W.to(DEV), Hd, 4, 64)
+    assert len(caplog.records) >= 1  # the escalation did run
+    # the dead columns hold w = 0 before quantization, as in the oracle
+    assert _agree(q[0, :, [17, 90]], rq[0, :, [17, 90]]) >= 0.98
+    assert _agree(q[0], rq[0]) >= 0.995
+    H_after = H.clone()
+    H_after[0, 17, 17] = H_after[0, 90, 90] = 1.0
+    assert torch.equal(Hd.cpu(), H_after)  # the dead-column fix in place, once
+    _check_vs(W, q, s, b, W_dq, rq, rs, rb, rW, H_after)
+    assert torch.allclose(rel.cpu(), rrel, rtol=1e-3, atol=0)
+
+
 def test_affine_batched_equals_per_item():
     """Reference tests/test_gptq.py:44-52 (bit-exact), affine mode."""
     from mlx_gptq import gptq

@@ -67,3 +67,25 @@ def test_oracle_choose_qparams_matches_reference(golden, bits, st):
     _, _, s32, b32 = grid_ref.choose_qparams(t["qparams.w"], bits, "mse", dt)
     assert torch.equal(s32, t[f"qparams.b{bits}.{st}.s32"])
     assert torch.equal(b32, t[f"qparams.b{bits}.{st}.b32"])
+
+
+@pytest.mark.parametrize("name", _cases())
+def test_oracle_dequantize_artifact_matches_reference_w_dq(golden, name):
+    """The reference's solver emits W_dq from the same codes and scales it
+    returns (grid.py:108-124 and 215-221 inside gptq.py's loops), so its
+    golden (q, scales, biases) triples pin the oracle's dequantize_artifact /
+    dequantize_mxfp (grid.py:127-139, 154-164) bit for bit: E2M1 and E4M3
+    decoding times 2^(byte-127) for the MXFP cases, q*s + b in fp32 for the
+    affine ones."""
+    t, meta = golden
+    kw = golden_io.case_kwargs(meta["cases"][name])
+    mode = kw.get("mode", "affine")
+    G = kw["group_size"]
+    q, s = t[f"{name}.q"], t[f"{name}.scales"]
+    b = t.get(f"{name}.biases")
+    dq = grid_ref.dequantize_artifact(q, s, b, mode, G)
+    assert dq.dtype == torch.float32
+    assert torch.equal(dq, t[f"{name}.W_dq"])
+    if mode != "affine":
+        dm = grid_ref.dequantize_mxfp(q, s, mode)
+        assert torch.equal(dm.reshape(q.shape), t[f"{name}.W_dq"])

@@ -349,3 +349,25 @@ def test_drop_expert_forgets_only_that_expert():
     assert st.token_counts().tolist() == [2, 1, 2]
     assert torch.equal(st.expert_rows(1), torch.ones(1, 4, dtype=torch.bfloat16))
     assert sorted(st.expert_rows(0)[:, 0].tolist()) == [0.0, 8.0]
+
+
+def test_clearing_one_sibling_view_keeps_the_other():
+    """Separate gate_proj / up_proj parameters share one RoutedStash; the
+    reference keeps one Stash per parameter and expert, and its clear() only
+    empties that one (capture.py:78-79, .tokens kept). Clearing gate's view
+    of expert e must leave up's rows of expert e in place."""
+    st = capture.RoutedStash("s", 4, 3)
+    x = torch.arange(12, dtype=torch.float32).reshape(3, 4)
+    st.add_routed(x, torch.tensor([[0, 1], [1, 2], [2, 0]]))
+    gate = capture.ExpertRows(st, 1, "m.gate_proj::e1")
+    up = capture.ExpertRows(st, 1, "m.up_proj::e1")
+    gate.clear()
+    assert gate.tokens == 2 and gate.chunks == [] and gate.nbytes() == 0
+    assert up.tokens == 2 and up.nbytes() == 2 * 4 * 2
+    assert sorted(up.chunks[0][:, 0].tolist()) == [0.0, 4.0]
+    assert st.token_counts().tolist() == [2, 2, 2]
+    up.clear()  # the last view of expert 1: its rows go
+    assert st.token_counts().tolist() == [2, 0, 2]
+    assert up.tokens == 2 and gate.tokens == 2  # .tokens kept, as the reference's
+    gate.clear()  # a second clear changes nothing
+    assert gate.tokens == 2
