@@ -50,7 +50,8 @@ def _args(argv=None):
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="time budget of the CPU-oracle sample (0 disables it)")
+                    help="time budget of the CPU-oracle sample of the dense configs; config 4 "
+                         "times its whole layer on the CPU (about 20 s); 0 disables the CPU leg")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="before the steps, run one plain elementwise copy (torch.neg) of this many "
                          "MiB: the reference dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE "
@@ -211,8 +212,12 @@ def run_moe(args, torch, np) -> int:
     # solver's output is still in the caches (the two are independent of the
     # other projection's work; packing the gate_up codes after the down
     # solve read them back from HBM at 2.5x the time).
+    # Every step plans its Hessian launches from scratch: a real calibration
+    # sees a new routing (new expert offsets) in every layer, so the plan
+    # cache of grouped_hessian would miss each time.
     def step():
         evs = _events(torch, 6)
+        capture.clear_hessian_plan_cache()
         evs[0].record()
         capture.grouped_hessian(L.X, L.offsets, L.row_index, out=H_gu, validate=False)
         evs[1].record()
@@ -236,7 +241,7 @@ def run_moe(args, torch, np) -> int:
     roofline = _roofline("syrk_kernel (gate_up Hessian, routed gather)", "mfma",
                          A * hidden * (hidden + 1),  # SYRK count N*C*(C+1)
                          float(phase[0]), _traffic("bench_moe_cfg4", "mgq::syrk_kernel<true"))
-    cpu = _cpu_baseline_moe(L, ne, out, args.cpu_seconds, (H_gu, H_dn)) if args.cpu_seconds > 0 else None
+    cpu = _cpu_baseline_moe(L, ne, out, (H_gu, H_dn)) if args.cpu_seconds > 0 else None
     config = {
         "workload": "cfg4 Qwen3-30B-A3B MoE layer: 128 experts x (gate_up [1536,2048] + down "
                     "[2048,768]), 131072 tokens top-8, MXFP4 safe-scale-search GPTQ, 4 unrouted "
@@ -247,12 +252,19 @@ def run_moe(args, torch, np) -> int:
     phases = {"hessian_gate_up": phase[0], "hessian_down": phase[1],
               "solve_and_pack_gate_up": phase[2], "solve_and_pack_down": phase[3],
               "rtn_and_pack_unrouted": phase[4]}
-    # rocprofv3 MFMA-busy / active cycles of the two SYRK launches (the
-    # profiler cannot run inside this process: committed per-dispatch figures)
-    counters = {"hessian_mfma_util_pct": {
-        "gate_up": _counter("bench_moe_cfg4", "mgq::syrk_kernel<true", "mfma_util_pct"),
-        "down": _counter("bench_moe_cfg4", "mgq::syrk_kernel<false", "mfma_util_pct")},
-        "solve_valu_busy_pct": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel", "valu_busy_pct")}
+    # rocprofv3 MFMA-busy / active cycles of the two SYRK launches and the
+    # solver's VALU-busy share. The profiler cannot run inside this process,
+    # so these are NOT measured by this run: they are read from the committed
+    # per-dispatch counters of an earlier profiled run of this workload.
+    counters = {"from_profile": {
+        "source": "profiles/bench_moe_cfg4_counters.json (rocprofv3 --pmc of bench.py, an "
+                  "earlier run; not measured in this run)",
+        "hessian_mfma_util_pct": {
+            "gate_up": _counter("bench_moe_cfg4", "mgq::syrk_kernel<true", "mfma_util_pct"),
+            "down": _counter("bench_moe_cfg4", "mgq::syrk_kernel<false", "mfma_util_pct")},
+        "solve_valu_busy_pct": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel",
+                                        "valu_busy_pct")},
+        "hessian_plan": "cold: planned and uploaded inside every timed step (new routing per layer)"}
     _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, counters)
     return 0
 
@@ -429,34 +441,16 @@ def _cpu_setup(torch) -> dict:
             "torch": torch.__version__, "mkl": bool(torch.backends.mkl.is_available())}
 
 
-def _block_diag_groups(H, groups):
-    """[B, 32k, 32k] with the diagonal 32x32 blocks of H for `groups` (the
-    only part of H an MXFP solve reads, gptq.py:99)."""
-    import torch
-
-    k = len(groups)
-    out = torch.zeros(H.shape[0], 32 * k, 32 * k, dtype=torch.float32)
-    for i, g in enumerate(groups):
-        out[:, 32 * i:32 * i + 32, 32 * i:32 * i + 32] = H[:, 32 * g:32 * g + 32, 32 * g:32 * g + 32].cpu()
-    return out
-
-
-def _cpu_baseline_moe(L, ne, gpu_out, budget_s, H_gpu):
+def _cpu_baseline_moe(L, ne, gpu_out, H_gpu):
     """The reference's path on the host CPU (the oracle: a torch-CPU
     restatement of capture.py:68-76, gptq.py and packing.py), in the shape
-    sequential.py:536-626 runs it: per-expert fp32 addmm Hessians, then ONE
-    stacked solve_gptq over all routed experts (the reference's span holds
-    all of them at its default 16 GiB budget), RTN for the unrouted experts
-    and numpy packing.
-
-    Bounded sample, extrapolated linearly: Hessians of whole experts until
-    half the budget is spent (cost per assignment x all assignments), and the
-    stacked solve over every routed expert on a subset of the 32-column
-    groups, which are independent and equal in cost (x groups / sampled
-    groups). RTN and packing are timed in full. Code agreement with the GPU
-    is measured on the sampled groups (the CPU solve gets the GPU's Hessian
-    blocks, so both see identical inputs)."""
-    import numpy as np
+    sequential.py:536-626 runs it, timed in full on the whole layer:
+    per-expert fp32 addmm Hessians of every routed expert, then ONE stacked
+    solve_gptq over all routed experts per projection (the reference's span
+    holds all of them at its default 16 GiB budget), RTN for the unrouted
+    experts and numpy packing. The stacked solves are given the GPU's
+    Hessians, so both sides solve identical inputs and their codes can be
+    compared element for element."""
     import torch
 
     sys.path.insert(0, ROOT)
@@ -467,42 +461,29 @@ def _cpu_baseline_moe(L, ne, gpu_out, budget_s, H_gpu):
     q_gu, _, q_dn, _, _ = gpu_out
     H_gu, H_dn = H_gpu
     A = L.offsets[ne]
-    # 1. Hessians, whole experts, spread over light and heavy ones
-    spent_h, done_a, n_exp = 0.0, 0, 0
-    for e in list(range(0, ne, 7)) + [e for e in range(ne) if e % 7]:
+    # 1. Hessians of every routed expert (rows gathered on the host first,
+    #    as the reference's CPU stashes hold them)
+    hess_s = 0.0
+    for e in range(ne):
         a, b = L.offsets[e], L.offsets[e + 1]
         xs = L.X.index_select(0, L.row_index[a:b].long()).cpu()
         ys = L.Y[a:b].cpu()
         t = time.perf_counter()
         hessian_ref.stash_hessian([xs], hidden)
         hessian_ref.stash_hessian([ys], inter)
-        spent_h += time.perf_counter() - t
-        done_a += b - a
-        n_exp += 1
-        if spent_h >= 0.5 * budget_s:
-            break
-    hess_s = spent_h * A / max(done_a, 1)
-    # 2. one stacked solve over all routed experts, on sampled groups
-    solve_s, agree_n, agree_d, sampled, partial = 0.0, 0, 0, [], n_exp < ne
-    for name, W, H, q_g in (("gate_up", L.W_gate_up, H_gu, q_gu), ("down", L.W_down, H_dn, q_dn)):
-        G = W.shape[2] // 32
-        per_group, k = 0.0, 0
-        for g in np.random.default_rng(0).permutation(G):
-            cols = slice(32 * g, 32 * g + 32)
-            Wc = W[:ne, :, cols].cpu()
-            Hc = _block_diag_groups(H[:ne], [g])
-            t = time.perf_counter()
-            rq, _, _, _, _ = gptq_ref.solve_gptq(Wc, Hc, 4, 32, mode="mxfp4")
-            per_group += time.perf_counter() - t
-            k += 1
-            agree_n += int((q_g[:, :, cols].cpu() == rq).sum())
-            agree_d += rq.numel()
-            if per_group >= 0.2 * budget_s:
-                break
-        solve_s += per_group * G / k
-        partial = partial or k < G
-        sampled.append(f"{name} {k}/{G} groups")
-    # 3. RTN of the unrouted experts and numpy packing of every code tensor, in full
+        hess_s += time.perf_counter() - t
+    # 2. one stacked MXFP4 safe-search solve per projection over all routed experts
+    solve_s, agree_n, agree_d = 0.0, 0, 0
+    for W, H, q_g in ((L.W_gate_up, H_gu, q_gu), (L.W_down, H_dn, q_dn)):
+        Wc = W[:ne].cpu()
+        Hc = H[:ne].cpu()
+        t = time.perf_counter()
+        rq, _, _, _, _ = gptq_ref.solve_gptq(Wc, Hc, 4, 32, mode="mxfp4")
+        solve_s += time.perf_counter() - t
+        agree_n += int((q_g.cpu() == rq).sum())
+        agree_d += rq.numel()
+        del Wc, Hc, rq
+    # 3. RTN of the unrouted experts and numpy packing of every code tensor
     t = time.perf_counter()
     rq_g, _, _, _ = grid_ref.rtn_quantize_mxfp(L.W_gate_up[ne:].cpu().float(), "mxfp4")
     rq_d, _, _, _ = grid_ref.rtn_quantize_mxfp(L.W_down[ne:].cpu().float(), "mxfp4")
@@ -516,14 +497,14 @@ def _cpu_baseline_moe(L, ne, gpu_out, budget_s, H_gpu):
         "unit": "elements/s",
         **info,
         "kind": "port",
-        "extrapolated": partial,
+        "extrapolated": False,
         "seconds": {"hessians": round(hess_s, 2), "solve": round(solve_s, 2),
                     "rtn_and_pack": round(tail_s, 2), "layer": round(total, 2)},
-        "sample": (f"Hessians of {n_exp}/{ne} routed experts ({done_a}/{A} assignments, fp32 addmm "
-                   f"over 65536-row chunks) x {A / max(done_a, 1):.2f}; one stacked MXFP4 "
-                   f"safe-search solve of all {ne} routed experts on {', '.join(sampled)} (groups "
-                   f"are independent, equal cost), scaled to all groups; RTN of the {L.experts - ne} "
-                   f"unrouted experts and numpy pack_q of the whole layer timed in full"),
+        "sample": (f"the whole layer, nothing extrapolated: fp32 addmm Hessians (65536-row "
+                   f"chunks) of all {ne} routed experts ({A} assignments, gate_up and down "
+                   f"inputs); one stacked MXFP4 safe-search solve_gptq of all {ne} routed experts "
+                   f"per projection, on the GPU's Hessians; RTN of the {L.experts - ne} unrouted "
+                   f"experts and numpy pack_q of every code tensor"),
         "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
     }
 

@@ -880,8 +880,22 @@ extern "C" int mgq_hessian_plan(int64_t C, int64_t n_groups, const int64_t* offs
   MGQ_REQUIRE(C >= 1 && n_groups >= 1, MGQ_ERR_SHAPE, "bad Hessian shape C=%lld groups=%lld",
               (long long)C, (long long)n_groups);
   MGQ_REQUIRE(offsets != nullptr, MGQ_ERR_VALUE, "offsets required");
-  Plan p;
-  if (int rc = build_plan(C, n_groups, offsets, target_items, &p)) return rc;
+  // A caller asks for the size first and then for the plan itself with the
+  // same arguments: the plan built for the size query is kept (per thread)
+  // and handed out by the second call instead of being built again.
+  thread_local Plan last;
+  thread_local std::vector<int64_t> last_key;
+  std::vector<int64_t> key(offsets, offsets + n_groups + 1);
+  key.push_back(C);
+  key.push_back(target_items);
+  if (key != last_key) {
+    last_key.clear();
+    Plan built;
+    if (int rc = build_plan(C, n_groups, offsets, target_items, &built)) return rc;
+    last = std::move(built);
+    last_key = std::move(key);
+  }
+  const Plan& p = last;
   const int64_t need = p.hdr.plan_bytes;
   if (plan_bytes) *plan_bytes = need;
   if (workspace_bytes)

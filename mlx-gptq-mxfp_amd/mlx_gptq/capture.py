@@ -117,6 +117,15 @@ def _hessian_plan(dev: torch.device, stream: int, C: int, off: np.ndarray, targe
     return plan, ws
 
 
+def clear_hessian_plan_cache() -> None:
+    """Forget every cached Hessian launch plan and its device workspace.
+    The next launch of each shape plans again, as the first launch for a new
+    routing (a new layer's offsets) does; the workspaces go back to torch's
+    allocator."""
+    with _ws_lock:
+        _WS_CACHE.clear()
+
+
 def grouped_hessian(
     X: torch.Tensor,
     offsets: Sequence[int] | np.ndarray | torch.Tensor,
