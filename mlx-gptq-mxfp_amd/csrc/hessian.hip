@@ -226,6 +226,7 @@ typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 typedef __attribute__((address_space(3))) char lds_char_t;
 constexpr int kTokB = 1024;  // LDS bytes per token: A row | B row
+constexpr int kRingWave = 512;  // a wave's index ring: 2 blocks of 64 int32
 
 __device__ inline bf16x8_t tr_frag(const lds_char_t* p) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
@@ -272,12 +273,16 @@ __global__ void __launch_bounds__(kThreads, 1)
   constexpr int L = (nks - 1) & 1;  // fragment buffer of a stage's last K-step
   constexpr int kDmaEvery = 8 / kDmaWave;  // one DMA every kDmaEvery MFMAs of segment 0
   static_assert(KB % 32 == 0 && kDmaWave <= 8 && (kDmaWave & (kDmaWave - 1)) == 0, "stage shape");
-  static_assert(NB * kStageB <= 160 * 1024, "LDS budget");
-  static_assert(!GATHER || NB == 2, "gathered row indices are loaded one stage ahead");
+  // Gathered launches with more than two stages take their row indices from
+  // an LDS ring (kRing, see idx_ring below); with two they load them one
+  // stage ahead into VGPRs.
+  constexpr bool kRing = GATHER && NB > 2;
+  static_assert(!kRing || kDmaWave == 4, "index ring blocks are 16 stages of 4 tokens");
+  static_assert(NB * kStageB + (kRing ? 8 * kRingWave : 0) <= 160 * 1024, "LDS budget");
   constexpr int kVm = (NB - 2) * kDmaWave;
   static_assert(kVm <= 63, "vmcnt range");
   constexpr int kWait = (kVm & 15) | ((kVm >> 4) << 14) | (7 << 4);
-  __shared__ __attribute__((aligned(1024))) char lds[NB * kStageB];
+  __shared__ __attribute__((aligned(1024))) char lds[NB * kStageB + (kRing ? 8 * kRingWave : 0)];
 
   const HessItem it = items[blockIdx.x];
   if (it.g < 0) return;
@@ -332,7 +337,7 @@ __global__ void __launch_bounds__(kThreads, 1)
   // token chunk. The loaded values are dead; they are kept live until the
   // stage barrier's vmcnt(0) so that their registers are not reused while a
   // load is in flight.
-  constexpr bool kPf = GATHER && !BIG;
+  constexpr bool kPf = GATHER && !BIG && !kRing;
   constexpr int kPfAhead = 1;
   const int nt = static_cast<int>((C + kTile - 1) / kTile);
   const int pf_parts = it.ti == it.tj ? 1 : 2;
@@ -372,11 +377,11 @@ __global__ void __launch_bounds__(kThreads, 1)
       return 0;
     }
   };
-  auto dma_i = [&](int i, uint32_t dst, int rem, int32_t idxv, const char* base) {
+  auto dma_i = [&](int i, uint32_t dst, int rem, int32_t idxv, const char* base, int lbase = 0) {
     const char* sa;
     uint32_t vo;
     if constexpr (GATHER) {
-      uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(idxv, i));
+      uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_readlane(idxv, lbase + i));
       r = r < nr1 ? r : nr1;
       if constexpr (BIG) {
         sa = Xb + static_cast<uint64_t>(r) * ldx2;
@@ -399,13 +404,64 @@ __global__ void __launch_bounds__(kThreads, 1)
   auto stage_base = [&](int64_t t0) -> const char* {
     return Xb + static_cast<uint64_t>(t0 < k1 ? t0 : k0) * ldx2;
   };
-  // this wave's DMAs of stage p (p < NB) before the loop
-  auto first_dmas = [&](int p, int32_t idxv) {
+  // this wave's DMAs of stage p (p < NB) before the loop; idxv lanes
+  // lbase.. hold the stage's row indices (gathered launches)
+  auto first_dmas = [&](int p, int32_t idxv, int lbase = 0) {
     const int64_t t0 = twave + p * KB;
     const int rem = stage_rem(t0);
     const char* base = stage_base(t0);
 #pragma unroll
-    for (int i = 0; i < kDmaWave; ++i) dma_i(i, lds_u32 + p * kStageB + wave_dst, rem, idxv, base);
+    for (int i = 0; i < kDmaWave; ++i)
+      dma_i(i, lds_u32 + p * kStageB + wave_dst, rem, idxv, base, lbase);
+  };
+
+  // Index ring (kRing). A wave's row indices come into LDS 64 at a time (16
+  // stages of 4 tokens) by one global_load_lds_dword, 15 iterations before
+  // their first use, into a ring of two blocks: block c holds the indices
+  // of stages NB + 16c .. NB + 16c + 15 and sits in slot c % 2; block c + 1 is
+  // fetched at iteration 16c, after the barrier that follows the last read
+  // of the block it replaces. Each iteration reads the next stage's 4
+  // indices from the ring with one ds_read_b32, a whole stage before its
+  // DMAs take them by v_readlane. Indices loaded into VGPRs would be vector
+  // loads, which complete in order: waiting for one would also wait for
+  // every row DMA issued before it, and the pipeline would drain.
+  const uint32_t ring = lds_u32 + NB * kStageB + wave * kRingWave;
+  auto ring_pos = [&](int st0) -> uint32_t {  // lane l: stage st0 + l / 4, token l % 4
+    const int64_t t = twave + static_cast<int64_t>(st0 + (lane >> 2)) * KB + (lane & 3);
+    return static_cast<uint32_t>(t < k1 ? t : k1 - 1);
+  };
+  auto ring_fetch = [&](int c) {  // block c into slot c % 2
+    const uint64_t a = reinterpret_cast<uint64_t>(row_index);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    const int32_t* sa = reinterpret_cast<const int32_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+                 :
+                 : "s"(ring + (c & 1) * 256), "v"(4 * ring_pos(NB + 16 * c)), "s"(sa)
+                 : "memory");
+  };
+  auto ring_read = [&](int st) -> int32_t {  // stage st's 4 indices in lanes 0..3 (and repeats)
+    const int c = (st - NB) >> 4;
+    const uint32_t a = ring - lds_u32 + (c & 1) * 256 + ((st - NB) & 15) * 16 + 4 * (lane & 3);
+    return *reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(lds3 + a);
+  };
+  // Prologue DMAs of stages 0 .. NB - 2; returns the indices of stage NB - 1
+  // (in lanes 4 (NB - 1)..) for its DMAs after the first barrier. The ring's
+  // first block is fetched before them, so the barrier's wait covers it.
+  auto prologue_dmas = [&](int32_t& idx_last, int& lb_last) {
+    if constexpr (kRing) {
+      const int32_t idx_pre = row_index[ring_pos(0)];  // stages 0 .. NB-1, lanes 0 .. 4 NB - 1
+      ring_fetch(0);
+#pragma unroll
+      for (int p = 0; p < NB - 1; ++p) first_dmas(p, idx_pre, 4 * p);
+      idx_last = idx_pre;
+      lb_last = 4 * (NB - 1);
+    } else {
+#pragma unroll
+      for (int p = 0; p < NB - 1; ++p) first_dmas(p, load_idx(twave + p * KB));
+      idx_last = load_idx(twave + (NB - 1) * KB);
+      lb_last = 0;
+    }
   };
 
   // The K loop of one wave: NM MFMAs per K-step into acc[NM], fragments at
@@ -419,14 +475,15 @@ __global__ void __launch_bounds__(kThreads, 1)
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
     if (n_stages <= 0) return;
     bf16x8_t fr[2][NR];
-#pragma unroll
-    for (int p = 0; p < NB - 1; ++p) first_dmas(p, load_idx(twave + p * KB));
-    int32_t idx_n = load_idx(twave + (NB - 1) * KB);
-    __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+    int32_t idx_n;
+    int lb_n;
+    prologue_dmas(idx_n, lb_n);
+    __builtin_amdgcn_s_waitcnt(GATHER && !kRing ? 0 : kWait);
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int qq = 0; qq < NR; ++qq) SYRK_READ(0, qq, 0u);
-    first_dmas(NB - 1, idx_n);
+    first_dmas(NB - 1, idx_n, lb_n);
+    if constexpr (kRing) idx_n = ring_read(NB);  // for iteration 0's DMAs (stage NB)
     __builtin_amdgcn_sched_barrier(0);
     int rbuf = 0;
     uint32_t pf_v = 0, pf_sink = 0;
@@ -440,7 +497,7 @@ __global__ void __launch_bounds__(kThreads, 1)
         for (int j = 0; j < NM; ++j) {
           SYRK_MFMA(P, j);
           if (j < NR) SYRK_READ(P ^ 1, j, rd + ks * 16 * kTokB);
-          if (GATHER && ks == 1 && j == 1)
+          if (GATHER && !kRing && ks == 1 && j == 1)
             idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
           if (kPf && ks == 1 && j == 2 && pf_wave) pf_idx = pf_index(s);
           __builtin_amdgcn_sched_barrier(0);
@@ -448,9 +505,14 @@ __global__ void __launch_bounds__(kThreads, 1)
       }
       const uint32_t wbuf = static_cast<uint32_t>(rbuf);
       rbuf = rbuf + 1 == NB ? 0 : rbuf + 1;
-      __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+      __builtin_amdgcn_s_waitcnt(GATHER && !kRing ? 0 : kWait);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
+      int32_t idx_next = 0;
+      if constexpr (kRing) {
+        if ((s & 15) == 0) ring_fetch((s >> 4) + 1);
+        idx_next = ring_read(s + NB + 1);
+      }
       const uint32_t nrd = static_cast<uint32_t>(rbuf * kStageB);
       const uint32_t dst = lds_u32 + wbuf * kStageB + wave_dst;
       const int64_t t0 = twave + static_cast<int64_t>(s + NB) * KB;
@@ -468,6 +530,7 @@ __global__ void __launch_bounds__(kThreads, 1)
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (kRing) idx_n = idx_next;
     }
     {
       const uint32_t rd = static_cast<uint32_t>(rbuf * kStageB);
@@ -496,25 +559,32 @@ __global__ void __launch_bounds__(kThreads, 1)
     if (h == 1 && diag) {
       // a single diagonal tile: the B half repeats the A half; DMAs only
       if (n_stages > 0) {
-#pragma unroll
-        for (int p = 0; p < NB - 1; ++p) first_dmas(p, load_idx(twave + p * KB));
-        int32_t idx_n = load_idx(twave + (NB - 1) * KB);
-        __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+        int32_t idx_n;
+        int lb_n;
+        prologue_dmas(idx_n, lb_n);
+        __builtin_amdgcn_s_waitcnt(GATHER && !kRing ? 0 : kWait);
         __builtin_amdgcn_s_barrier();
-        first_dmas(NB - 1, idx_n);
+        first_dmas(NB - 1, idx_n, lb_n);
+        if constexpr (kRing) idx_n = ring_read(NB);
         int rbuf = 0;
         for (int s = 0; s < n_stages - 1; ++s) {
-          idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
+          if constexpr (!kRing) idx_n = load_idx(twave + static_cast<int64_t>(s + NB) * KB);
           const uint32_t wbuf = static_cast<uint32_t>(rbuf);
           rbuf = rbuf + 1 == NB ? 0 : rbuf + 1;
-          __builtin_amdgcn_s_waitcnt(GATHER ? 0 : kWait);
+          __builtin_amdgcn_s_waitcnt(GATHER && !kRing ? 0 : kWait);
           __builtin_amdgcn_s_barrier();
+          int32_t idx_next = 0;
+          if constexpr (kRing) {
+            if ((s & 15) == 0) ring_fetch((s >> 4) + 1);
+            idx_next = ring_read(s + NB + 1);
+          }
           const int64_t t0 = twave + static_cast<int64_t>(s + NB) * KB;
           const int rem = stage_rem(t0);
           const char* base = stage_base(t0);
 #pragma unroll
           for (int i = 0; i < kDmaWave; ++i)
             dma_i(i, lds_u32 + wbuf * kStageB + wave_dst, rem, idx_n, base);
+          if constexpr (kRing) idx_n = idx_next;
         }
         __builtin_amdgcn_s_waitcnt(0);
       }
@@ -946,12 +1016,22 @@ extern "C" int mgq_hessian(const void* X, int64_t n_rows, int64_t ldx, int64_t C
     if (int rc = check_launch("hessian zero row")) return rc;
     const dim3 grid(static_cast<unsigned>(h.n_items));
     const uint16_t* Xh = static_cast<const uint16_t*>(X);
+    const char* gs = getenv("MGQ_HESSIAN_GATHER_STAGES");
+    const bool two_stage = gs != nullptr && strcmp(gs, "2") == 0;
     if (row_index && wide_gather_addr(n_rows, ldx)) {
-      syrk_kernel<true, true, 64, 2><<<grid, kThreads, 0, s>>>(
-          Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
+      if (two_stage)
+        syrk_kernel<true, true, 64, 2><<<grid, kThreads, 0, s>>>(
+            Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
+      else
+        syrk_kernel<true, true, 32, 4><<<grid, kThreads, 0, s>>>(
+            Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
     } else if (row_index) {
-      syrk_kernel<true, false, 64, 2><<<grid, kThreads, 0, s>>>(
-          Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
+      if (two_stage)
+        syrk_kernel<true, false, 64, 2><<<grid, kThreads, 0, s>>>(
+            Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
+      else
+        syrk_kernel<true, false, 32, 4><<<grid, kThreads, 0, s>>>(
+            Xh, n_rows, ldx, C, row_index, items, H, partials, accumulate, zero_row);
     } else {
       syrk_kernel<false, false, 32, 4><<<grid, kThreads, 0, s>>>(
           Xh, n_rows, ldx, C, nullptr, items, H, partials, accumulate, zero_row);
