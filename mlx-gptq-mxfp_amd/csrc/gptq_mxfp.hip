@@ -541,7 +541,7 @@ __global__ void __launch_bounds__(kThreads)
       for (int k0 = 0; k0 < c; k0 += 4) {
         const f32x4_t u4 = *reinterpret_cast<const lds_f32x4*>(col + k0);
 #pragma unroll
-        for (int k = k0; k < c && k < k0 + 4; ++k) acc = acc - errs[k] * u4[k - k0];
+        for (int k = k0; k < c && k < k0 + 4; ++k) acc = fmaf(-errs[k], u4[k - k0], acc);
       }
       float dq;
       const uint32_t code = quant_exact<MODE, !EXACT>(acc, inv_scale, scale, &dq);
