@@ -15,7 +15,8 @@
 //      quadratic form err^T Hg err, strict '<' so the first best wins;
 //   2. 32-step GPTQ with the chosen fixed scale:
 //        dq_c = Q(w_c);  err = (w_c - dq_c) / U[c,c];  w_j -= err * U[c,j] (j>c)
-//      (sub, IEEE div, mul, sub: the exact torch op sequence);
+//      (sub and IEEE div as torch does them; the update w_j -= err * U[c,j]
+//      as one fused multiply-add, where torch rounds the product first);
 //   3. safe search keeps the GPTQ result only if its objective <= the best
 //      RTN candidate's;
 //   4. range guard: every |dq| <= max(32 * max|orig|, 2^-126), else the RTN
@@ -511,8 +512,12 @@ __global__ void __launch_bounds__(kThreads)
   // reference updates all later columns after each step
   // (W[c+1:] -= err_c * U[c, c+1:]); each element therefore sees
   // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
-  // Forming w_c lazily from the stored errors performs exactly those
-  // roundings while keeping only err[] live.
+  // Forming w_c lazily from the stored errors keeps that order while keeping
+  // only err[] live. Each step is one fused multiply-add (the reference
+  // rounds err_k U[k,c] before subtracting it): half the instructions of the
+  // two-op form, and the codes it gives agree with the reference's on
+  // practically every element (none differed on a 12.6 M-code sample of the
+  // config-4 layer).
   //
   // The divisions take Markstein's correction without a branch (EXACT =
   // false; copysign gives a zero numerator its own zero) and only record the
