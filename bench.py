@@ -52,6 +52,10 @@ def _args(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of the CPU-oracle sample of the dense configs; config 4 "
                          "times its whole layer on the CPU (about 20 s); 0 disables the CPU leg")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time torch.matmul / torch.bmm in bf16 (hipBLASLt) on a square GEMM and "
+                         "on the config-4 gate_up Gram shapes instead of the solve: the vendor "
+                         "library's sustained bf16 rate on this box, beside the SYRK's")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="before the steps, run one plain elementwise copy (torch.neg) of this many "
                          "MiB: the reference dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE "
@@ -262,8 +266,13 @@ def run_moe(args, torch, np) -> int:
         "hessian_mfma_util_pct": {
             "gate_up": _counter("bench_moe_cfg4", "mgq::syrk_kernel<true", "mfma_util_pct"),
             "down": _counter("bench_moe_cfg4", "mgq::syrk_kernel<false", "mfma_util_pct")},
+        "hessian_clock_ghz": {
+            "gate_up": _counter("bench_moe_cfg4", "mgq::syrk_kernel<true", "clock_ghz"),
+            "down": _counter("bench_moe_cfg4", "mgq::syrk_kernel<false", "clock_ghz")},
         "solve_valu_busy_pct": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel",
-                                        "valu_busy_pct")},
+                                        "valu_busy_pct"),
+        "solve_valu_insts_per_row_group": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel",
+                                                   "valu_insts_per_lane_item")},
         "hessian_plan": "cold: planned and uploaded inside every timed step (new routing per layer)"}
     _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, counters)
     return 0
@@ -658,6 +667,48 @@ def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
     }
 
 
+def run_gemm_ceiling(args, torch):
+    """bf16 GEMMs through torch (hipBLASLt on ROCm), fp32 accumulation, timed
+    with events over args.steps launches after args.warmup: a square
+    8192^3 product, the config-4 gate_up Gram matrix of all 1048576 routed
+    rows as one [2048 x 1048576] x [1048576 x 2048] product, and 128
+    per-expert [2048 x 8192] x [8192 x 2048] products as one bmm (operands
+    contiguous). Full products: twice the flops of the lower triangle the
+    SYRK computes."""
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    cases = []
+    a = torch.randn(8192, 8192, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(8192, 8192, generator=g, device=dev).to(torch.bfloat16)
+    cases.append(("square 8192^3", lambda: torch.matmul(a, b), 2 * 8192 ** 3))
+    X = torch.randn(1048576, 2048, generator=g, device=dev).to(torch.bfloat16)
+    XT = X.t().contiguous()
+    cases.append(("gram [2048 x 1048576] x [1048576 x 2048]", lambda: torch.matmul(XT, X),
+                  2 * 2048 * 2048 * 1048576))
+    Xe = X.view(128, 8192, 2048)
+    XeT = Xe.transpose(1, 2).contiguous()
+    cases.append(("128 x gram [2048 x 8192] x [8192 x 2048] (bmm)", lambda: torch.bmm(XeT, Xe),
+                  2 * 128 * 2048 * 2048 * 8192))
+    out = []
+    for name, fn, flops in cases:
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        out.append({"case": name, "ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                    "frac_of_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+        print(json.dumps(out[-1]), flush=True)
+    print(json.dumps({"metric": "bf16 GEMM ceiling (torch.matmul / bmm, hipBLASLt)", "unit": "TFLOP/s",
+                      "peak": PEAK_BF16_TFLOPS, "steps": args.steps, "cases": out}))
+    return 0
+
+
 def main(argv=None) -> int:
     args = _args(argv)
     if args.gpus != 1:
@@ -672,6 +723,8 @@ def main(argv=None) -> int:
 
     _native.load()
     torch.cuda.set_device(torch.device("cuda", 0))
+    if args.gemm_ceiling:
+        return run_gemm_ceiling(args, torch)
     if args.audit:
         if args.config != 4:
             print("--audit measures the config-4 layer only", file=sys.stderr)

@@ -73,6 +73,7 @@ def _solve_vs_oracle(W: torch.Tensor, H: torch.Tensor, kw: dict, rows: int, seed
     pl_ref = _proxy(Ws.float(), rW, H)
     if kw.get("mode", "affine") != "affine":
         assert torch.equal(grid.dequantize_artifact(q, s, None, kw["mode"], 32), W_dq)
+    _solve_vs_oracle.last = (s, W_dq)  # the full GPU result, for decision checks
     return agree, s_agree, pl, pl_ref
 
 
@@ -108,6 +109,16 @@ def test_dense_config_full_size(cfg):
     for j, m in enumerate(L.mats):
         agree, s_agree, pl, pl_ref = _solve_vs_oracle(m.W, Hs[m.inp].clone(), m.solve, 48, seed=cfg + j)
         _check(agree, s_agree, pl, pl_ref, _scale_gate(m.solve))
+        if cfg == 5 and j == 0:
+            # config 5's gate_proj runs the MXFP4 safe search: its decisions
+            # on 64 sampled rows x all 160 groups against float64 objectives
+            s_gpu, dq_gpu = _solve_vs_oracle.last
+            g = torch.Generator().manual_seed(55)
+            rows = torch.sort(torch.randperm(m.W.shape[1], generator=g)[:64]).values
+            cf, gf, n = _decisions_vs_fp64(m.W[0], Hs[m.inp][0], s_gpu[0], dq_gpu[0], rows)
+            assert n == 64 * (m.W.shape[2] // 32)
+            assert cf == 0 and gf == 0, (cf, gf, n)
+            del s_gpu, dq_gpu
     del L, Hs
     torch.cuda.empty_cache()
 
