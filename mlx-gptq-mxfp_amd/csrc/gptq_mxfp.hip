@@ -298,6 +298,22 @@ __device__ inline float decode_code(uint32_t word, int k) {
   }
 }
 
+// The recurrence's fast-pass MXFP4 encode (mx4_encode_hw_nonan) of one
+// column, written straight into byte k of its codes word: the conversion
+// stores the code and a zero code in that byte and keeps the other three,
+// so no shift and merge is needed; dq is decoded from the same byte.
+__device__ inline float mx4_encode_into(uint32_t& word, int k, float w, float inv_scale,
+                                        float scale) {
+  const float n = w * inv_scale + 0.0f;  // -0 -> +0, as mx4_encode_hw_nonan
+  switch (k) {
+    case 0: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 0); break;
+    case 1: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 1); break;
+    case 2: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 2); break;
+    default: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 3); break;
+  }
+  return decode_code<kMxfp4>(word, k) * scale;
+}
+
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 
 // The 32 weights of one (row, group), 16-byte loads, widened to fp32.
@@ -536,11 +552,15 @@ __global__ void __launch_bounds__(kThreads)
     float mag_hi = 0.0f;
 #pragma unroll
     for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
+    // Ut's base, passed from column to column through lds_after so that its
+    // register is updated in place (no copy per column) and every column's
+    // reads take immediate offsets from it
+    const lds_f32* ubase = (const lds_f32*)Ut;
 #pragma unroll
     for (int c = 0; c < kG; ++c) {
       // column c of U (row c of Ut, 16-byte aligned), read 4 values at a time
-      const lds_f32* col = (const lds_f32*)Ut + c * kG;
-      if (c) col = lds_after(col, errs[c - 1]);
+      if (c) ubase = lds_after(ubase, errs[c - 1]);
+      const lds_f32* col = ubase + c * kG;
       float acc = ORIG(c);
 #pragma unroll
       for (int k0 = 0; k0 < c; k0 += 4) {
@@ -549,7 +569,11 @@ __global__ void __launch_bounds__(kThreads)
         for (int k = k0; k < c && k < k0 + 4; ++k) acc = fmaf(-errs[k], u4[k - k0], acc);
       }
       float dq;
-      const uint32_t code = quant_exact<MODE, !EXACT>(acc, inv_scale, scale, &dq);
+      uint32_t code = 0u;
+      if constexpr (MODE == kMxfp4 && !EXACT)
+        dq = mx4_encode_into(codes[c / 4], c % 4, acc, inv_scale, scale);
+      else
+        code = quant_exact<MODE, !EXACT>(acc, inv_scale, scale, &dq);
       const float a = acc - dq;  // errs[c] = a / U[c][c]
       if constexpr (EXACT) {
         errs[c] = div_exact(a, col[c], ydiag[c]);
@@ -559,7 +583,7 @@ __global__ void __launch_bounds__(kThreads)
         mag_lo = min(mag_lo, (f2u(a) << 1) - 2u);
         mag_hi = fmaxf(mag_hi, fabsf(a));
       }
-      codes[c / 4] |= code << (8 * (c % 4));
+      if constexpr (!(MODE == kMxfp4 && !EXACT)) codes[c / 4] |= code << (8 * (c % 4));
       dq_set(c, dq);
     }
     return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f) |
