@@ -277,23 +277,25 @@ __device__ inline const lds_f32* lds_after(const lds_f32* p, float dep) {
   return reinterpret_cast<const lds_f32*>(static_cast<uintptr_t>(a));
 }
 
-// value(code) of the code in byte k of `word` (one code per byte), on the
-// hardware decode at scale 1 (k is a constant once the callers unroll).
+// value(code) * scale of the code in byte k of `word` (one code per byte),
+// on the hardware decode with the E8M0 scale passed in, which equals the
+// decode at scale 1 times the scale bit for bit (k is a constant once the
+// callers unroll).
 template <int MODE>
-__device__ inline float decode_code(uint32_t word, int k) {
+__device__ inline float decode_code(uint32_t word, int k, float scale) {
   if constexpr (MODE == kMxfp4) {
     switch (k) {
-      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 0)[0];
-      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 1)[0];
-      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 2)[0];
-      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, 3)[0];
+      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 0)[0];
+      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 1)[0];
+      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 2)[0];
+      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 3)[0];
     }
   } else {
     switch (k) {
-      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, false)[0];
-      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, false)[1];
-      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, true)[0];
-      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, true)[1];
+      case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, scale, false)[0];
+      case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, scale, false)[1];
+      case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, scale, true)[0];
+      default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, scale, true)[1];
     }
   }
 }
@@ -311,7 +313,7 @@ __device__ inline float mx4_encode_into(uint32_t& word, int k, float w, float in
     case 2: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 2); break;
     default: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 3); break;
   }
-  return decode_code<kMxfp4>(word, k) * scale;
+  return decode_code<kMxfp4>(word, k, scale);
 }
 
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
@@ -479,7 +481,7 @@ __global__ void __launch_bounds__(kThreads)
     if constexpr (!SAFE)
       return dqr[i];
     else
-      return decode_code<MODE>(codes[i / 4], i % 4) * dq_scale;
+      return decode_code<MODE>(codes[i / 4], i % 4, dq_scale);
   };
   auto dq_set = [&](int i, float v) __attribute__((always_inline)) {
     if constexpr (!SAFE) dqr[i] = v;

@@ -83,13 +83,18 @@ __device__ inline float mx8_clamp_limit(float scale) {
   return fminf(448.0f * scale, 3.40282347e38f);
 }
 
+// The encoders below take scale = 2^e, e in [-127, 127] (an E8M0 scale), and
+// inv_scale = 2^-e. Their dq is the decode with the scale passed to the
+// conversion, which equals value(code) * scale bit for bit for every code and
+// every such scale (tests/test_gpu_mx_hw.py checks all of them).
+//
 // Exact MXFP4 code and dq = value(code) * scale of n = w * inv_scale
 // (= mx4_encode for every fp32 w).
 __device__ inline uint32_t mx4_encode_hw(float w, float inv_scale, float scale, float* dq) {
   const float n = w * inv_scale;
   uint32_t code = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, n, 0.0f, 1.0f, 0);
   code = (n == 0.0f || n != n) ? 0u : code;
-  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, 1.0f, 0)[0] * scale;
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, scale, 0)[0];
   return code;
 }
 
@@ -101,7 +106,7 @@ __device__ inline uint32_t mx4_encode_hw(float w, float inv_scale, float scale, 
 __device__ inline uint32_t mx4_encode_hw_nonan(float w, float inv_scale, float scale, float* dq) {
   const float n = w * inv_scale + 0.0f;
   const uint32_t code = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, n, 0.0f, 1.0f, 0);
-  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, 1.0f, 0)[0] * scale;
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, scale, 0)[0];
   return code;
 }
 
@@ -113,7 +118,7 @@ __device__ inline uint32_t mx8_encode_hw(float w, float inv_scale, float scale, 
   const mx_s16x2_t p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(mx_s16x2_t{0, 0}, c, 0.0f, 1.0f, false);
   uint32_t code = __builtin_bit_cast(uint32_t, p);
   code = (n != n) ? (((f2u(n) >> 24) & 0x80u) | 0x7fu) : code;
-  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0] * scale;
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, scale, false)[0];
   return code;
 }
 
@@ -124,7 +129,7 @@ __device__ inline uint32_t mx8_encode_hw_nonan(float w, float inv_scale, float s
   const float c = __builtin_amdgcn_fmed3f(n, -448.0f, 448.0f);
   const mx_s16x2_t p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(mx_s16x2_t{0, 0}, c, 0.0f, 1.0f, false);
   const uint32_t code = __builtin_bit_cast(uint32_t, p);
-  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0] * scale;
+  *dq = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, scale, false)[0];
   return code;
 }
 

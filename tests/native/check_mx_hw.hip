@@ -17,6 +17,13 @@
 //   7  MXFP8 error not exact in bf16 although w is a bf16 value and
 //      2^-126 <= |n| < 16384
 //
+// mgq_hwcheck_scaled_decode(counts): the scaled decodes with the scale
+// folded in against the decode at scale 1 times the scale, bit for bit
+// (NaN == NaN), for every byte value in every byte position and every
+// E8M0 scale 2^e, e in [-127, 127]:
+//   counts[0]: v_cvt_scalef32_pk_f32_fp4 (both values of the byte)
+//   counts[1]: v_cvt_scalef32_pk_f32_fp8 (both halves)
+//
 // mgq_hwcheck_div(stride_log, counts): div_exact(a, d, div_exact_recip(d))
 // against a / d, bit for bit:
 //   counts[0]: a, d over all significands in [1, 2), d every 2^stride_log-th
@@ -131,6 +138,32 @@ __global__ void div_ranges_kernel(unsigned long long* counts) {
 
 }  // namespace
 
+// Block e + 127, thread = byte value b, replicated into all four bytes.
+__global__ void scaled_decode_kernel(unsigned long long* counts) {
+  const int e = static_cast<int>(blockIdx.x) - 127;
+  const float scale = exp2_int(e);
+  const uint32_t word = threadIdx.x * 0x01010101u;
+  unsigned long long bad4 = 0, bad8 = 0;
+#define MGQ_CHECK4(k)                                                           \
+  {                                                                             \
+    const auto a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, k);   \
+    const auto b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, k);    \
+    bad4 += !same_bits(a[0], b[0] * scale) + !same_bits(a[1], b[1] * scale);   \
+  }
+  MGQ_CHECK4(0) MGQ_CHECK4(1) MGQ_CHECK4(2) MGQ_CHECK4(3)
+#undef MGQ_CHECK4
+#define MGQ_CHECK8(h)                                                           \
+  {                                                                             \
+    const auto a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, scale, h);   \
+    const auto b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, h);    \
+    bad8 += !same_bits(a[0], b[0] * scale) + !same_bits(a[1], b[1] * scale);   \
+  }
+  MGQ_CHECK8(false) MGQ_CHECK8(true)
+#undef MGQ_CHECK8
+  if (bad4) atomicAdd(&counts[0], bad4);
+  if (bad8) atomicAdd(&counts[1], bad8);
+}
+
 // Runs the MX check for scale exponent e in [-127, 127]; counts: host array of 8.
 extern "C" int mgq_hwcheck_mx(int e, unsigned long long* counts) {
   if (e < -127 || e > 127) return -1;
@@ -140,6 +173,18 @@ extern "C" int mgq_hwcheck_mx(int e, unsigned long long* counts) {
   check_kernel<<<(1u << 22) / 256, 256>>>(e, d);
   hipError_t err = hipDeviceSynchronize();
   if (err == hipSuccess) err = hipMemcpy(counts, d, kKinds * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  hipFree(d);
+  return err == hipSuccess ? 0 : -3;
+}
+
+// Runs the scaled-decode check; counts: host array of 2.
+extern "C" int mgq_hwcheck_scaled_decode(unsigned long long* counts) {
+  unsigned long long* d = nullptr;
+  if (hipMalloc(&d, 2 * sizeof(unsigned long long)) != hipSuccess) return -2;
+  hipMemset(d, 0, 2 * sizeof(unsigned long long));
+  scaled_decode_kernel<<<255, 256>>>(d);
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemcpy(counts, d, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
   hipFree(d);
   return err == hipSuccess ? 0 : -3;
 }

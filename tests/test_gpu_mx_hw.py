@@ -60,3 +60,21 @@ def test_markstein_division_matches_ieee():
     counts = (ctypes.c_ulonglong * 2)()
     assert lib.mgq_hwcheck_div(6, counts) == 0
     assert list(counts) == [0, 0]
+
+
+def test_scaled_decode_folds_the_scale_exactly():
+    """v_cvt_scalef32_pk_f32_fp4 / _fp8 with the E8M0 scale passed in equal
+    the decode at scale 1 times the scale, bit for bit, for every byte
+    value, byte position and scale 2^-127 .. 2^127: the solver's dq
+    (value(code) * scale, grid.py's dequantize) may take the scale in the
+    conversion."""
+    import torch
+
+    assert torch.cuda.is_available()
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} missing: run build() first")
+    lib = ctypes.CDLL(LIB)
+    lib.mgq_hwcheck_scaled_decode.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    counts = (ctypes.c_ulonglong * 2)()
+    assert lib.mgq_hwcheck_scaled_decode(counts) == 0
+    assert (int(counts[0]), int(counts[1])) == (0, 0), (int(counts[0]), int(counts[1]))
