@@ -538,7 +538,9 @@ __global__ void __launch_bounds__(kThreads)
   // config-4 layer).
   //
   // The divisions take Markstein's correction without a branch (EXACT =
-  // false; copysign gives a zero numerator its own zero) and only record the
+  // false; a zero numerator may come out as a zero of either sign, which no
+  // output can see: errors only feed the later columns' sums, and a zero sum
+  // of either sign encodes to code 0 and decodes to +0) and only record the
   // numerators' range: their smallest nonzero magnitude (as a bit pattern
   // shifted left by one, minus 2, so that a zero wraps to the top) and their
   // largest. If one fell outside the correction's exact range, or a NaN
@@ -581,7 +583,7 @@ __global__ void __launch_bounds__(kThreads)
         errs[c] = div_exact(a, col[c], ydiag[c]);
       } else {
         const float y = ydiag[c], q = a * y;
-        errs[c] = copysignf(fmaf(fmaf(-q, col[c], a), y, q), a);
+        errs[c] = fmaf(fmaf(-q, col[c], a), y, q);
         mag_lo = min(mag_lo, (f2u(a) << 1) - 2u);
         mag_hi = fmaxf(mag_hi, fabsf(a));
       }
