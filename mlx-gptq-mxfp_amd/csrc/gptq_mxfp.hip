@@ -596,6 +596,11 @@ __global__ void __launch_bounds__(kThreads)
   if (ydiag_zero || __builtin_amdgcn_ballot_w64(recurrence(std::false_type{})) != 0)
     recurrence(std::true_type{});
 
+  // The GPTQ result's dequantized values, decoded once for the objective
+  // below, the range guard and the stores.
+  float w[kG];
+#pragma unroll
+  for (int i = 0; i < kG; ++i) w[i] = DQ(i);
   // 3. GPTQ vs best RTN candidate (safe search only)
   bool use_gptq = true;
   if (SAFE) {
@@ -603,7 +608,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int i0 = 0; i0 < kG; i0 += 8) {
 #pragma unroll
-      for (int i = i0; i < i0 + 8; ++i) err[i] = (DQ(i) - ORIG(i)) * inv_scale;
+      for (int i = i0; i < i0 + 8; ++i) err[i] = (w[i] - ORIG(i)) * inv_scale;
       __builtin_amdgcn_sched_barrier(0);
     }
     use_gptq = mfma_objective(err, hs, lane) * exp2_int(2 * (e_sel - e0)) <= best;
@@ -615,7 +620,7 @@ __global__ void __launch_bounds__(kThreads)
   bool ok = use_gptq;
   if (use_gptq) {
 #pragma unroll
-    for (int i = 0; i < kG; ++i) ok = ok & (fabsf(DQ(i)) <= limit);  // no short-circuit branches
+    for (int i = 0; i < kG; ++i) ok = ok & (fabsf(w[i]) <= limit);  // no short-circuit branches
   }
   if (!ok) {  // RTN baseline at the chosen scale
 #pragma unroll
@@ -625,12 +630,9 @@ __global__ void __launch_bounds__(kThreads)
       float dq;
       const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
       codes[i / 4] |= code << (8 * (i % 4));
-      dq_set(i, dq);
+      w[i] = dq;
     }
   }
-  float w[kG];
-#pragma unroll
-  for (int i = 0; i < kG; ++i) w[i] = DQ(i);
 
   double num = 0.0, den_d = 0.0;
   if (valid) {
