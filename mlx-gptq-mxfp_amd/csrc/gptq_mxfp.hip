@@ -516,7 +516,7 @@ __global__ void __launch_bounds__(kThreads)
         __builtin_amdgcn_sched_barrier(0);
       }
       const float raw = XERR ? mfma_objective_x1(err, hs, lane) : mfma_objective(err, hs, lane);
-      const float obj = raw * exp2_int(2 * (e - e0));
+      const float obj = __builtin_amdgcn_ldexpf(raw, 2 * (e - e0));
       if (o == 0 || obj < best) {
         best = obj;
         e_sel = e;
@@ -611,7 +611,7 @@ __global__ void __launch_bounds__(kThreads)
       for (int i = i0; i < i0 + 8; ++i) err[i] = (w[i] - ORIG(i)) * inv_scale;
       __builtin_amdgcn_sched_barrier(0);
     }
-    use_gptq = mfma_objective(err, hs, lane) * exp2_int(2 * (e_sel - e0)) <= best;
+    use_gptq = __builtin_amdgcn_ldexpf(mfma_objective(err, hs, lane), 2 * (e_sel - e0)) <= best;
   }
   // 4. range guard on the selected result
   float limit = amax * 32.0f;

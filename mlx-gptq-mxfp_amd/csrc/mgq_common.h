@@ -101,11 +101,9 @@ __device__ inline int e8m0_exponent(float max_abs, float fmax) {
   return r > 127 ? 127 : r;
 }
 
-// 2^k for k in [-127, 127] (exact; 2^-127 is subnormal), like torch.pow(2, k).
-__device__ inline float exp2_int(int k) {
-  if (k >= -126) return __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
-  return __uint_as_float(0x00400000u);  // 2^-127
-}
+// 2^k for k in [-127, 127] (exact; 2^-127 is subnormal), like torch.pow(2, k):
+// one v_ldexp_f32 (fp32 denormals are kept in this build's float mode).
+__device__ inline float exp2_int(int k) { return __builtin_amdgcn_ldexpf(1.0f, k); }
 
 // ---------------------------------------------------------------------------
 // E2M1 (grid.py:82-105): saturating round-half-even onto
