@@ -785,8 +785,21 @@ std::vector<std::pair<int32_t, int32_t>> pair_diagonals(
 int build_plan(int64_t C, int64_t n_groups, const int64_t* offsets, int64_t target_items,
                Plan* plan) {
   const int64_t nt = ceil_div(C, kTile);
-  const auto tiles = pair_diagonals(blocked_tiles(nt));
+  auto tiles = pair_diagonals(blocked_tiles(nt));
   const int64_t T = static_cast<int64_t>(tiles.size());
+  // A group whose items fit one round of an XCD (32 CUs) runs them side by
+  // side, so their order only decides which CUs free up first: the costlier
+  // items go first (a diagonal pair, 18 MFMAs per K-step on its busiest
+  // SIMD, then the off-diagonal tiles, 16, then a lone diagonal tile, 10),
+  // so that the next group's items fill the CUs that finish early. Larger
+  // groups keep the super-block order, which their rounds' L2 reuse needs.
+  if (T <= kCUs / kXcds) {
+    auto cost = [](const std::pair<int32_t, int32_t>& t) {
+      return t.first < t.second ? 18 : (t.first > t.second ? 16 : 10);
+    };
+    std::stable_sort(tiles.begin(), tiles.end(),
+                     [&](const auto& a, const auto& b) { return cost(a) > cost(b); });
+  }
   int64_t active = 0, n_max = 0, total_tokens = 0;
   for (int64_t g = 0; g < n_groups; ++g) {
     const int64_t n = offsets[g + 1] - offsets[g];
