@@ -274,6 +274,22 @@ def run_moe(args, torch, np) -> int:
         "solve_valu_insts_per_row_group": _counter("bench_moe_cfg4", "mgq::mxfp_solve_kernel",
                                                    "valu_insts_per_lane_item")},
         "hessian_plan": "cold: planned and uploaded inside every timed step (new routing per layer)"}
+    # every phase against its own bound: the SYRKs against bf16 MFMA, the
+    # solve + pack phases against HBM with their algorithmic bytes (bf16 W in,
+    # f32 W_dq + u8 code + E8M0 scale out, then the codes read and packed)
+    el_gu = ne * 2 * inter * hidden
+    el_dn = ne * hidden * inter
+    per_el = MXFP_BYTES_PER_ELEMENT + 1 + 0.5
+    counters["phase_rooflines"] = {
+        "hessian_gate_up": roofline,
+        "hessian_down": _roofline("syrk_kernel (down Hessian, expert rows)", "mfma",
+                                  A * inter * (inter + 1), float(phase[1]),
+                                  _traffic("bench_moe_cfg4", "mgq::syrk_kernel<false")),
+        "solve_and_pack_gate_up": _roofline("MXFP4 safe-search solve + pack (gate_up)", "hbm",
+                                            el_gu * per_el, float(phase[2])),
+        "solve_and_pack_down": _roofline("MXFP4 safe-search solve + pack (down)", "hbm",
+                                         el_dn * per_el, float(phase[3])),
+    }
     _line(args, value, ms_step, config, phases, roofline, cpu, setup_s, counters)
     return 0
 
