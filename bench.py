@@ -21,9 +21,11 @@ Inputs (hidden states, routing, weights) are synthetic, seeded, and
 resident in HBM before the timed region. One step = one layer. The JSON
 line reports weight elements solved per second, the dominant kernel against
 its roofline, and the CPU oracle (the reference algorithm restated on
-torch-CPU) timed on a bounded sample of the same workload.
+torch-CPU) timed on the same workload: in full for configs 1-4, in full
+for config 5 but for its down-proj Hessian, which is timed on 65536 of its
+524288 tokens and scaled linearly in tokens.
 
-Usage: python bench.py [--config 4] [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+Usage: python bench.py [--config 4] [--gpus 1] [--steps K] [--warmup W] [--cpu-sample] [--cpu-seconds S]
 """
 
 from __future__ import annotations
@@ -50,8 +52,14 @@ def _args(argv=None):
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="time budget of the CPU-oracle sample of the dense configs; config 4 "
-                         "times its whole layer on the CPU (about 20 s); 0 disables the CPU leg")
+                    help="time budget of the CPU-oracle sample taken with --cpu-sample; "
+                         "0 disables the CPU leg")
+    ap.add_argument("--cpu-sample", action="store_true",
+                    help="dense configs: time the CPU oracle on a bounded sample of about "
+                         "--cpu-seconds and scale it, instead of the whole layer. Without it "
+                         "every part is timed in full except a Hessian above 2e14 dense flops "
+                         "(config 5's 25600-wide down input, about 8 minutes on the host), "
+                         "timed on 65536 tokens and scaled linearly in tokens")
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="time torch.matmul / torch.bmm in bf16 (hipBLASLt) on a square GEMM and "
                          "on the config-4 gate_up Gram shapes instead of the solve: the vendor "
@@ -610,7 +618,8 @@ def run_dense(args, torch, np) -> int:
     if dom.startswith("hessian_"):
         # the profile's largest SYRK dispatch is the dominant Hessian
         rooflines[dom]["traffic"] = _traffic(tag, "mgq::syrk_kernel<false")
-    cpu = _cpu_baseline_dense(L, out[:2], out[2], args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = (_cpu_baseline_dense(L, out[:2], out[2], args.cpu_seconds, not args.cpu_sample)
+           if args.cpu_seconds > 0 else None)
     config = {"workload": L.name, "elements": elements,
               "matrices": {m.name: list(m.W.shape[1:]) for m in L.mats},
               "tokens": {k: int(X.shape[0]) for k, X in L.inputs.items()}}
@@ -628,12 +637,14 @@ def run_dense(args, torch, np) -> int:
     return 0
 
 
-def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
-    """CPU oracle on a bounded sample, extrapolated linearly: the Hessian on
-    the first tokens of each input (its cost is linear in tokens) and the
-    solve + pack on the first rows of each matrix with the full Hessian (the
-    column loops are elementwise over rows; the O(C^3) Cholesky of the affine
-    path is timed once and not scaled)."""
+def _cpu_baseline_dense(L, gpu_out, Hs, budget_s, full=True):
+    """CPU oracle on the whole layer (full) or on a bounded sample scaled
+    linearly. full: every Hessian whose dense count 2 N C^2 is at most 2e14
+    flops on all its tokens, a larger one on its first 65536 tokens (its cost
+    is linear in tokens), every solve + pack on all rows. Sampled: each
+    Hessian on the first tokens that fit the budget and each solve + pack on
+    the first 2048 rows with the full Hessian (the column loops are
+    elementwise over rows); the affine path always solves all rows."""
     import torch
 
     sys.path.insert(0, ROOT)
@@ -643,42 +654,47 @@ def _cpu_baseline_dense(L, gpu_out, Hs, budget_s):
     res, _ = gpu_out
     t_total, agree_n, agree_d, parts = 0.0, 0, 0, []
     per_budget = budget_s / (len(L.inputs) + len(L.mats))
+    sampled = False
     for k, X in L.inputs.items():
         N, C = X.shape
-        n_s = int(min(N, max(256, per_budget * 0.9e12 / (2.0 * C * C))))
+        if full and 2.0 * N * C * C <= 2e14:
+            n_s = N
+        elif full:  # a 65536-token sample, scaled linearly in tokens
+            n_s = min(N, 65536)
+        else:
+            n_s = int(min(N, max(256, per_budget * 0.9e12 / (2.0 * C * C))))
+        sampled |= n_s < N
         xs = X[:n_s].cpu()
         t = time.perf_counter()
         hessian_ref.stash_hessian([xs], C)
         dt = time.perf_counter() - t
         t_total += dt * N / n_s
         parts.append(f"Hessian '{k}' on {n_s}/{N} tokens")
+        print(f"cpu leg: {parts[-1]}: {dt:.1f} s", file=sys.stderr, flush=True)
     for m, r in zip(L.mats, res):
         R, C = m.W.shape[1:]
         kw = dict(m.solve)
         H = Hs[m.inp].cpu()
-        hinv_t = 0.0
-        if kw["mode"] == "affine":  # the full-matrix factor is per layer, not per row
-            t = time.perf_counter()
-            gptq_ref.prepare_hinv(H.clone(), 0.01)
-            hinv_t = time.perf_counter() - t
-        r_s = R if kw["mode"] == "affine" else int(min(R, 2048))
+        r_s = R if (kw["mode"] == "affine" or full) else int(min(R, 2048))
+        sampled |= r_s < R
         Ws = m.W[0, :r_s].unsqueeze(0).cpu()
         t = time.perf_counter()
         rq = gptq_ref.solve_gptq(Ws, H.clone(), **kw)[0]
         packing_ref.pack_q(rq[0].numpy(), m.pack_bits)
         dt = time.perf_counter() - t
-        t_total += hinv_t + max(dt - hinv_t, 0.0) * R / r_s
+        t_total += dt * R / r_s
         agree_n += int((r[0][0, :r_s].cpu() == rq[0]).sum())
         agree_d += rq.numel()
         parts.append(f"solve+pack '{m.name}' on {r_s}/{R} rows")
+        print(f"cpu leg: {parts[-1]}: {dt:.1f} s", file=sys.stderr, flush=True)
     return {
         "value": round(L.elements / t_total, 1),
         "unit": "elements/s",
         **info,
         "kind": "port",
-        "extrapolated": True,
-        "sample": "CPU oracle, extrapolated linearly from " + "; ".join(parts)
-                  + f" (estimated {t_total:.1f} s per layer)",
+        "extrapolated": sampled,
+        "sample": ("CPU oracle, extrapolated linearly from " if sampled else "CPU oracle, timed in full: ")
+                  + "; ".join(parts) + f" ({'estimated ' if sampled else ''}{t_total:.1f} s per layer)",
         "code_agreement_with_gpu": round(agree_n / max(agree_d, 1), 6),
     }
 
