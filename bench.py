@@ -220,10 +220,9 @@ def run_moe(args, torch, np) -> int:
 
     H_gu = torch.empty(E, hidden, hidden, dtype=torch.float32, device=dev)
     H_dn = torch.empty(E, inter, inter, dtype=torch.float32, device=dev)
-    # Each projection's codes are packed right after its solve, while the
-    # solver's output is still in the caches (the two are independent of the
-    # other projection's work; packing the gate_up codes after the down
-    # solve read them back from HBM at 2.5x the time).
+    # Each projection's codes are packed by its solve (packed_out: the
+    # solver writes pack_q's words from the codes it holds), so they are not
+    # read back from HBM by a separate packing pass.
     # Every step plans its Hessian launches from scratch: a real calibration
     # sees a new routing (new expert offsets) in every layer, so the plan
     # cache of grouped_hessian would miss each time.
@@ -235,11 +234,13 @@ def run_moe(args, torch, np) -> int:
         evs[1].record()
         capture.grouped_hessian(L.Y, L.offsets, out=H_dn)
         evs[2].record()
-        q_gu, s_gu, _, wq_gu, _ = gptq.solve_gptq(L.W_gate_up[:ne], H_gu[:ne], 4, 32, mode="mxfp4")
-        p_gu = packing.pack_q(q_gu, 4)
+        p_gu = torch.empty(ne, 2 * inter, hidden // 8, dtype=torch.int32, device=dev)
+        q_gu, s_gu, _, wq_gu, _ = gptq.solve_gptq(L.W_gate_up[:ne], H_gu[:ne], 4, 32, mode="mxfp4",
+                                                  packed_out=p_gu)
         evs[3].record()
-        q_dn, s_dn, _, wq_dn, _ = gptq.solve_gptq(L.W_down[:ne], H_dn[:ne], 4, 32, mode="mxfp4")
-        p_dn = packing.pack_q(q_dn, 4)
+        p_dn = torch.empty(ne, hidden, inter // 8, dtype=torch.int32, device=dev)
+        q_dn, s_dn, _, wq_dn, _ = gptq.solve_gptq(L.W_down[:ne], H_dn[:ne], 4, 32, mode="mxfp4",
+                                                  packed_out=p_dn)
         evs[4].record()
         rq_gu, rs_gu, _, _ = grid.rtn_quantize_mxfp(L.W_gate_up[ne:], "mxfp4")
         rq_dn, rs_dn, _, _ = grid.rtn_quantize_mxfp(L.W_down[ne:], "mxfp4")
@@ -284,10 +285,10 @@ def run_moe(args, torch, np) -> int:
         "hessian_plan": "cold: planned and uploaded inside every timed step (new routing per layer)"}
     # every phase against its own bound: the SYRKs against bf16 MFMA, the
     # solve + pack phases against HBM with their algorithmic bytes (bf16 W in,
-    # f32 W_dq + u8 code + E8M0 scale out, then the codes read and packed)
+    # f32 W_dq + u8 code + E8M0 scale + the packed 4-bit code out)
     el_gu = ne * 2 * inter * hidden
     el_dn = ne * hidden * inter
-    per_el = MXFP_BYTES_PER_ELEMENT + 1 + 0.5
+    per_el = MXFP_BYTES_PER_ELEMENT + 0.5
     counters["phase_rooflines"] = {
         "hessian_gate_up": roofline,
         "hessian_down": _roofline("syrk_kernel (down Hessian, expert rows)", "mfma",
@@ -546,7 +547,7 @@ def _cpu_baseline_moe(L, ne, gpu_out, H_gpu):
 # configs 1, 2, 3, 5: dense layers
 # ---------------------------------------------------------------------------
 def run_dense(args, torch, np) -> int:
-    from mlx_gptq import capture, gptq, packing, synth
+    from mlx_gptq import capture, gptq, synth
 
     dev = torch.device("cuda", 0)
     t_setup = time.perf_counter()
@@ -563,7 +564,12 @@ def run_dense(args, torch, np) -> int:
         L.inputs[k] = st.chunks[0]  # the stash's copy; the generated one is freed
         stashes[k] = st
     torch.cuda.synchronize()
-    n_ev = len(keys) + len(L.mats) + 1
+    n_ev = len(keys) + len(L.mats)
+    # each matrix's codes packed by its solve (packed_out), as pack_q would
+    def packed_shape(m):
+        B_, R_, C_ = m.W.shape
+        return (B_, R_, C_ * m.pack_bits // 32)
+
     def step():
         evs = _events(torch, n_ev + 1)
         i = 0
@@ -573,14 +579,12 @@ def run_dense(args, torch, np) -> int:
             Hs[k] = stashes[k].hessian(dev).unsqueeze(0)
             i += 1
             evs[i].record()
-        res = []
+        res, packed = [], []
         for m in L.mats:
-            res.append(gptq.solve_gptq(m.W, Hs[m.inp], **m.solve))
+            packed.append(torch.empty(packed_shape(m), dtype=torch.int32, device=dev))
+            res.append(gptq.solve_gptq(m.W, Hs[m.inp], **m.solve, packed_out=packed[-1]))
             i += 1
             evs[i].record()
-        packed = [packing.pack_q(r[0], m.pack_bits) for r, m in zip(res, L.mats)]
-        i += 1
-        evs[i].record()
         return (res, packed, Hs), evs
 
     _copy_calibration(torch, dev, args.copy_calib_mib)
@@ -596,7 +600,7 @@ def run_dense(args, torch, np) -> int:
                                               N * C * (C + 1), float(phase[i]))
     for j, m in enumerate(L.mats):
         ms = float(phase[len(keys) + j])
-        phases[f"solve_{m.name}"] = ms
+        phases[f"solve_and_pack_{m.name}"] = ms
         n = int(m.W.numel())
         if m.solve["mode"] == "affine":
             # O(C^3) work: the fp64 factor + inverse (2C^3/3 algorithmic, potrf +
@@ -606,14 +610,14 @@ def run_dense(args, torch, np) -> int:
             R_, C_ = m.W.shape[-2], m.W.shape[-1]
             bs = 128
             upd = sum(2 * R_ * min(bs, C_ - i) * (C_ - min(i + bs, C_)) for i in range(0, C_, bs))
-            rooflines[f"solve_{m.name}"] = _roofline(
-                f"GPTQ solve '{m.name}' (affine: fp64 Cholesky-inverse + column loop + fp32 lazy update)",
-                "fp64", 2 * C_ ** 3 / 3 + upd, ms)
+            rooflines[f"solve_and_pack_{m.name}"] = _roofline(
+                f"GPTQ solve + pack '{m.name}' (affine: fp64 Cholesky-inverse + column loop + "
+                f"fp32 lazy update)", "fp64", 2 * C_ ** 3 / 3 + upd, ms)
             continue
-        byt = n * MXFP_BYTES_PER_ELEMENT
-        rooflines[f"solve_{m.name}"] = _roofline(f"GPTQ solve '{m.name}' ({m.solve['mode']})", "hbm",
-                                                 byt, ms)
-    phases["pack"] = phase[-1]
+        # bf16 W in; f32 W_dq, u8 code, E8M0 scale and the packed code out
+        byt = n * (MXFP_BYTES_PER_ELEMENT + m.pack_bits / 8)
+        rooflines[f"solve_and_pack_{m.name}"] = _roofline(
+            f"GPTQ solve + pack '{m.name}' ({m.solve['mode']})", "hbm", byt, ms)
     dom = max(rooflines, key=lambda k: rooflines[k]["launch_ms"])
     if dom.startswith("hessian_"):
         # the profile's largest SYRK dispatch is the dominant Hessian

@@ -244,6 +244,18 @@ int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_
                         uint8_t* scales_out, float* W_dq, float* rel_err, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* mgq_gptq_mxfp_solve followed by packing.py:15-26 pack_q of its codes
+ * (what sequential.py / pack.py do with a solved projection's q), in the
+ * solver's own launch: packed_out (u32 [B, R, C / 8] for mxfp4, [B, R, C / 4]
+ * for mxfp8, 16-byte aligned) receives exactly mgq_pack_q(q_out, bits), and
+ * the codes are not read back from HBM by a separate packing pass. Every
+ * other argument and result as mgq_gptq_mxfp_solve. */
+int mgq_gptq_mxfp_solve_packed(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
+                               int mode, int algorithm, const int32_t* offsets, int n_offsets,
+                               uint8_t* q_out, uint32_t* packed_out, uint8_t* scales_out,
+                               float* W_dq, float* rel_err, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* Allocation-free variant of mgq_gptq_mxfp. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -356,7 +356,8 @@ __global__ void __launch_bounds__(kThreads)
                       const float* __restrict__ Hc, const float* __restrict__ U,
                       const uint8_t* __restrict__ dead,
                       Offsets offs, uint8_t* __restrict__ q_out, uint8_t* __restrict__ s_out,
-                      float* __restrict__ W_dq, double* __restrict__ rel_part) {
+                      float* __restrict__ W_dq, double* __restrict__ rel_part,
+                      uint32_t* __restrict__ packed_out) {
   static_assert(!XERR || (SAFE && sizeof(TIn) == 2 && !IS_F16), "XERR needs bf16 weights");
   const int64_t G = C / kG;
   const int64_t chunks = (R + kThreads - 1) / kThreads;
@@ -639,6 +640,28 @@ __global__ void __launch_bounds__(kThreads)
     uint4* qp = reinterpret_cast<uint4*>(q_out + base);
     qp[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
     qp[1] = make_uint4(codes[4], codes[5], codes[6], codes[7]);
+    if (packed_out != nullptr) {
+      // the codes in MLX's uint32 layout (packing.py:15-26: value j of a
+      // word at bits width * j, LSB first): MXFP4 packs the 32 codes of the
+      // group into words 4g..4g+3 of the row, MXFP8's words are its code
+      // bytes as they are
+      if constexpr (MODE == kMxfp4) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          // byte 0 of t = codes 0 | 1 << 4, byte 2 = codes 2 | 3 << 4
+          const uint32_t t0 = codes[2 * p] | (codes[2 * p] >> 4);
+          const uint32_t t1 = codes[2 * p + 1] | (codes[2 * p + 1] >> 4);
+          pw[p] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
+        }
+        *reinterpret_cast<uint4*>(packed_out + (b * R + r) * (C / 8) + g * 4) =
+            make_uint4(pw[0], pw[1], pw[2], pw[3]);
+      } else {
+        uint4* pp = reinterpret_cast<uint4*>(packed_out + (b * R + r) * (C / 4) + g * 8);
+        pp[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+        pp[1] = make_uint4(codes[4], codes[5], codes[6], codes[7]);
+      }
+    }
     float4* op = reinterpret_cast<float4*>(W_dq + base);
 #pragma unroll
     for (int i = 0; i < kG / 4; ++i)
@@ -726,13 +749,13 @@ WsLayout ws_layout(int64_t B, int64_t R, int64_t C) {
 template <typename TIn, bool IS_F16, bool XERR>
 int launch_solve(const void* W, int64_t B, int64_t R, int64_t C, const float* Hc, const float* U,
                  const uint8_t* dead, int mode, bool safe, const Offsets& offs, uint8_t* q,
-                 uint8_t* s, float* W_dq, double* rel_part, hipStream_t st) {
+                 uint8_t* s, float* W_dq, double* rel_part, uint32_t* packed, hipStream_t st) {
   const int64_t G = C / kG;
   const int64_t blocks = B * G * ((R + kThreads - 1) / kThreads);
   const TIn* w = static_cast<const TIn*>(W);
 #define MGQ_LAUNCH(MODE, SAFE, X)                                                                    \
   mxfp_solve_kernel<TIn, IS_F16, MODE, SAFE, X><<<static_cast<unsigned>(blocks), kThreads, 0, st>>>( \
-      w, B, R, C, Hc, U, dead, offs, q, s, W_dq, rel_part)
+      w, B, R, C, Hc, U, dead, offs, q, s, W_dq, rel_part, packed)
   if constexpr (XERR) {
     if (mode == kMxfp4) MGQ_LAUNCH(kMxfp4, true, true); else MGQ_LAUNCH(kMxfp8, true, true);
   } else if (mode == kMxfp4) {
@@ -778,12 +801,15 @@ extern "C" int mgq_gptq_mxfp_prepare(float* H, int64_t B, int64_t R, int64_t C, 
   return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st);
 }
 
-extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
-                                   int mode, int algorithm, const int32_t* offsets, int n_offsets,
-                                   uint8_t* q_out, uint8_t* scales_out, float* W_dq,
-                                   float* rel_err, void* workspace, int64_t workspace_bytes,
-                                   void* stream) {
-  clear_error();
+namespace mgq {
+namespace {
+
+// mgq_gptq_mxfp_solve, and with packed_out != nullptr also the codes packed
+// as pack_q (packing.py:15-26) packs them, by the solver itself.
+int solve_entry(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C, int mode,
+                int algorithm, const int32_t* offsets, int n_offsets, uint8_t* q_out,
+                uint32_t* packed_out, uint8_t* scales_out, float* W_dq, float* rel_err,
+                void* workspace, int64_t workspace_bytes, void* stream) {
   MGQ_REQUIRE(mode == kMxfp4 || mode == kMxfp8, MGQ_ERR_VALUE, "not a microscaling mode: %d",
               mode);
   MGQ_REQUIRE(algorithm == 0 || algorithm == 1, MGQ_ERR_VALUE,
@@ -808,8 +834,9 @@ extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_
               "rel_err needs W_dq separate from W (in-place solves skip rel_err)");
   MGQ_REQUIRE((reinterpret_cast<uintptr_t>(W) & 15u) == 0 &&
                   (reinterpret_cast<uintptr_t>(W_dq) & 15u) == 0 &&
-                  (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0,
-              MGQ_ERR_SHAPE, "W, W_dq and q_out must be 16-byte aligned");
+                  (reinterpret_cast<uintptr_t>(q_out) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(packed_out) & 15u) == 0,
+              MGQ_ERR_SHAPE, "W, W_dq, q_out and packed_out must be 16-byte aligned");
   if (B == 0 || C == 0 || R == 0) return MGQ_OK;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
@@ -825,18 +852,19 @@ extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_
   for (int i = 0; i < offs.n; ++i) min_off = offs.v[i] < min_off ? offs.v[i] : min_off;
   const bool xerr = algorithm == 1 && w_dtype == kBF16 && min_off >= (mode == kMxfp4 ? -5 : -4);
   int rc;
+  double* rp = rel_err ? rel_part : nullptr;
   if (w_dtype == kF32) {
-    rc = launch_solve<float, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
-                                           scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<float, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs,
+                                           q_out, scales_out, W_dq, rp, packed_out, st);
   } else if (w_dtype == kBF16 && xerr) {
     rc = launch_solve<uint16_t, false, true>(W, B, R, C, Hcmp, U, dead, mode, true, offs, q_out,
-                                             scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+                                             scales_out, W_dq, rp, packed_out, st);
   } else if (w_dtype == kBF16) {
-    rc = launch_solve<uint16_t, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs,
-                                              q_out, scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<uint16_t, false, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1,
+                                              offs, q_out, scales_out, W_dq, rp, packed_out, st);
   } else {
-    rc = launch_solve<uint16_t, true, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1, offs, q_out,
-                                             scales_out, W_dq, rel_err ? rel_part : nullptr, st);
+    rc = launch_solve<uint16_t, true, false>(W, B, R, C, Hcmp, U, dead, mode, algorithm == 1,
+                                             offs, q_out, scales_out, W_dq, rp, packed_out, st);
   }
   if (rc) return rc;
   if (rel_err) {
@@ -845,6 +873,31 @@ extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_
     if (int rc2 = check_launch("rel_err")) return rc2;
   }
   return MGQ_OK;
+}
+
+}  // namespace
+}  // namespace mgq
+
+extern "C" int mgq_gptq_mxfp_solve(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,
+                                   int mode, int algorithm, const int32_t* offsets, int n_offsets,
+                                   uint8_t* q_out, uint8_t* scales_out, float* W_dq,
+                                   float* rel_err, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  return solve_entry(W, w_dtype, B, R, C, mode, algorithm, offsets, n_offsets, q_out, nullptr,
+                     scales_out, W_dq, rel_err, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mgq_gptq_mxfp_solve_packed(const void* W, int w_dtype, int64_t B, int64_t R,
+                                          int64_t C, int mode, int algorithm,
+                                          const int32_t* offsets, int n_offsets, uint8_t* q_out,
+                                          uint32_t* packed_out, uint8_t* scales_out, float* W_dq,
+                                          float* rel_err, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  clear_error();
+  MGQ_REQUIRE(packed_out != nullptr, MGQ_ERR_VALUE, "packed_out required");
+  return solve_entry(W, w_dtype, B, R, C, mode, algorithm, offsets, n_offsets, q_out, packed_out,
+                     scales_out, W_dq, rel_err, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,

@@ -82,8 +82,10 @@ def _prepare_hinv(H: torch.Tensor, damp: float, max_attempts: int = 6) -> torch.
 
 
 def _mxfp_solve(W_in: torch.Tensor, H: torch.Tensor, mode: str, damp: float, algorithm: str,
-                W_out: torch.Tensor, want_rel: bool):
+                W_out: torch.Tensor, want_rel: bool, packed: torch.Tensor | None = None):
     """Launch the fused MXFP solver; returns (q, scales, rel|None).
+    packed (u32/i32 [B, R, C * bits / 32], bits 4 for mxfp4 and 8 for mxfp8):
+    also filled with pack_q(q, bits) (packing.py:15-26) by the solver.
 
     The damped Cholesky-inverse runs first (mgq_gptq_mxfp_prepare); its
     per-block attempt counts are copied to pinned host memory before the
@@ -109,12 +111,15 @@ def _mxfp_solve(W_in: torch.Tensor, H: torch.Tensor, mode: str, damp: float, alg
              ws.data_ptr(), ws.numel(), stream)
 
     def solve():
-        nat.call(
-            "mgq_gptq_mxfp_solve", W_in.data_ptr(), nat.dtype_code(W_in.dtype), B, R, C,
-            nat.mode_code(mode), 1 if algorithm == "safe-scale-search" else 0,
-            ctypes.addressof(offs_arr), len(offs), q.data_ptr(), scales.data_ptr(), W_out.data_ptr(),
-            None if rel is None else rel.data_ptr(), ws.data_ptr(), ws.numel(), stream,
-        )
+        head = (W_in.data_ptr(), nat.dtype_code(W_in.dtype), B, R, C, nat.mode_code(mode),
+                1 if algorithm == "safe-scale-search" else 0, ctypes.addressof(offs_arr), len(offs),
+                q.data_ptr())
+        tail = (scales.data_ptr(), W_out.data_ptr(), None if rel is None else rel.data_ptr(),
+                ws.data_ptr(), ws.numel(), stream)
+        if packed is None:
+            nat.call("mgq_gptq_mxfp_solve", *head, *tail)
+        else:
+            nat.call("mgq_gptq_mxfp_solve_packed", *head, packed.data_ptr(), *tail)
 
     if W_out.data_ptr() == W_in.data_ptr():
         att_h = att.cpu().numpy()
@@ -258,12 +263,21 @@ def solve_gptq(
     storage_dtype: torch.dtype = torch.bfloat16,
     mode: str = "affine",
     mxfp_algorithm: str = "auto",
+    *,
+    packed_out: torch.Tensor | None = None,
 ):
     """Keep W_orig intact, return (q, scales, biases, W_dq, rel_err[B]) (gptq.py:275-302).
 
     Host tensors are solved on the current HIP device; every output is
     returned on W_orig's device and H gets the dead-column fix in place,
-    as the reference's device-agnostic torch code does."""
+    as the reference's device-agnostic torch code does.
+
+    packed_out (keyword only, not in the reference's signature): a
+    contiguous uint32 / int32 tensor [B, out, in * pack_bits / 32] on the
+    solving device, filled with ``packing.pack_q(q, pack_bits)``
+    (packing.py:15-26), pack_bits 4 for mxfp4, 8 for mxfp8 and ``bits`` for
+    the affine modes. The MXFP solver writes it from the codes it holds,
+    so the codes are not read back for a separate packing pass."""
     out_dev = W_orig.device
     if mode in ("mxfp4", "mxfp8"):
         assert W_orig.dim() == 3 and H.dim() == 3
@@ -279,8 +293,10 @@ def solve_gptq(
             else torch.float32
         src, H_d = _staged(W_orig, H, wdt)
         _require_device(src, H_d)
+        if packed_out is not None:
+            _check_packed(packed_out, (B, R, C), 4 if mode == "mxfp4" else 8, src.device)
         W_dq = torch.empty(B, R, C, dtype=torch.float32, device=src.device)
-        q, s, rel = _mxfp_solve(src, H_d, mode, damp, mxfp_algorithm, W_dq, True)
+        q, s, rel = _mxfp_solve(src, H_d, mode, damp, mxfp_algorithm, W_dq, True, packed_out)
         if H_d is not H:
             H.copy_(H_d)
         return q.to(out_dev), s.to(out_dev), None, W_dq.to(out_dev), rel.to(out_dev)
@@ -311,4 +327,20 @@ def solve_gptq(
     rel = gptq_affine.rel_err(W_dq, W0)
     if H_d is not H:
         H.copy_(H_d)
+    if packed_out is not None:
+        _check_packed(packed_out, (B, R, C), bits, q.device)
+        nat.call("mgq_pack_q", q.data_ptr(), B * R, C, bits, packed_out.data_ptr(),
+                 nat.stream_of(q.device))
     return q.to(out_dev), s.to(out_dev), b.to(out_dev), W_dq.to(out_dev), rel.to(out_dev)
+
+
+def _check_packed(packed: torch.Tensor, shape, pack_bits: int, dev) -> None:
+    B, R, C = shape
+    if pack_bits not in (2, 4, 8) or C % (32 // pack_bits):
+        raise ValueError(f"cannot pack {pack_bits}-bit codes of {C} columns for MLX")
+    want = (B, R, C * pack_bits // 32)
+    if (packed.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32))
+            or tuple(packed.shape) != want or not packed.is_contiguous()
+            or packed.device != dev or packed.data_ptr() % 16):
+        raise ValueError(f"packed_out must be a contiguous 16-byte aligned uint32 / int32 "
+                         f"tensor {list(want)} on {dev}")

@@ -376,3 +376,49 @@ def test_one_call_entry_point_equals_prepare_then_solve():
     torch.cuda.synchronize()
     assert torch.equal(q, q1) and torch.equal(s, s1) and torch.equal(wq, wq1)
     assert torch.equal(rel, rel1) and bool((att == 1).all())
+
+
+@pytest.mark.parametrize("mode,alg,wdt", [("mxfp4", "safe-scale-search", torch.bfloat16),
+                                          ("mxfp4", "safe-scale-search", torch.float32),
+                                          ("mxfp4", "groupwise", torch.float16),
+                                          ("mxfp8", "groupwise", torch.bfloat16),
+                                          ("mxfp8", "safe-scale-search", torch.float32)])
+def test_packed_out_equals_pack_q_of_the_codes(mode, alg, wdt):
+    """solve_gptq(..., packed_out=) (mgq_gptq_mxfp_solve_packed): the solver's
+    packed words are packing.pack_q of its codes bit for bit (and the oracle's
+    pack_q, packing.py:15-26), every other output equal to the unpacked
+    call's; rows past a workgroup's 256 (R = 300) and B = 3 included."""
+    from mlx_gptq import gptq, packing
+    from oracle import packing_ref
+
+    W, H, _ = _setup(B=3, R=300, C=192, N=1024, seed=21, scale=0.03)
+    bits = 4 if mode == "mxfp4" else 8
+    Wd = W.to(wdt).to(DEV)
+    q1, s1, _, wq1, rel1 = gptq.solve_gptq(Wd, H.clone().to(DEV), bits, 32, mode=mode,
+                                           mxfp_algorithm=alg)
+    packed = torch.full((3, 300, 192 * bits // 32), -1, dtype=torch.int32, device=DEV)
+    q2, s2, _, wq2, rel2 = gptq.solve_gptq(Wd, H.clone().to(DEV), bits, 32, mode=mode,
+                                           mxfp_algorithm=alg, packed_out=packed)
+    assert torch.equal(q1, q2) and torch.equal(s1, s2) and torch.equal(wq1, wq2)
+    assert torch.equal(rel1, rel2)
+    want = packing.pack_q(q2, bits)
+    assert torch.equal(packed.cpu().view(torch.int32), want.cpu().view(torch.int32))
+    ref = packing_ref.pack_q(q2.cpu().numpy(), bits)
+    assert np.array_equal(packed.cpu().numpy().view(np.uint32), ref)
+
+
+def test_packed_out_affine_and_bad_shapes():
+    """The affine path fills packed_out with pack_q(q, bits) too; a packed_out
+    of the wrong shape or dtype is refused before any launch."""
+    from mlx_gptq import gptq, packing
+
+    W, H, _ = _setup(B=1, R=64, C=128, N=1024, seed=23, scale=0.03)
+    packed = torch.empty(1, 64, 128 * 4 // 32, dtype=torch.int32, device=DEV)
+    q, *_ = gptq.solve_gptq(W.to(DEV), H.clone().to(DEV), 4, 64, packed_out=packed)
+    assert torch.equal(packed.cpu().view(torch.int32), packing.pack_q(q, 4).cpu().view(torch.int32))
+    for bad in (torch.empty(1, 64, 15, dtype=torch.int32, device=DEV),
+                torch.empty(1, 64, 16, dtype=torch.int64, device=DEV),
+                torch.empty(1, 64, 32, dtype=torch.int32, device=DEV)[..., ::2]):
+        with pytest.raises(ValueError, match="packed_out"):
+            gptq.solve_gptq(W.to(torch.bfloat16).to(DEV), H.clone().to(DEV), 4, 32, mode="mxfp4",
+                            packed_out=bad)
