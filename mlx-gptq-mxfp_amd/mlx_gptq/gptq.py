@@ -307,6 +307,8 @@ def solve_gptq(
     B, R, C = W0.shape
     assert H_d.shape == (B, C, C)
     assert C % group_size == 0, f"in_features {C} not divisible by group {group_size}"
+    if packed_out is not None:
+        _check_packed(packed_out, (B, R, C), bits, W0.device)
     # W is a private copy, so the column loop may start before the first
     # damped pass is known to have succeeded; if it had not, solve again from
     # a fresh copy on the synchronous path (escalation, warnings, errors).
@@ -328,7 +330,6 @@ def solve_gptq(
     if H_d is not H:
         H.copy_(H_d)
     if packed_out is not None:
-        _check_packed(packed_out, (B, R, C), bits, q.device)
         nat.call("mgq_pack_q", q.data_ptr(), B * R, C, bits, packed_out.data_ptr(),
                  nat.stream_of(q.device))
     return q.to(out_dev), s.to(out_dev), b.to(out_dev), W_dq.to(out_dev), rel.to(out_dev)

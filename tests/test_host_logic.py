@@ -40,3 +40,25 @@ def test_no_cpu_fallback_without_gpu():
         grid.rtn_quantize_mxfp(torch.zeros(2, 64), "mxfp4")
     with pytest.raises(RuntimeError, match="HIP devices only"):
         packing.pack_q(np.zeros((2, 8), dtype=np.uint8), 4)
+
+
+def test_packed_out_validation():
+    """solve_gptq's packed_out is checked for shape, dtype, layout, device and
+    alignment before any launch (gptq._check_packed), for the pack widths
+    pack_q accepts (packing.py:15-26)."""
+    from mlx_gptq import gptq
+
+    dev = torch.device("cpu")
+    ok = torch.zeros(2, 3, 64 * 4 // 32, dtype=torch.int32)
+    gptq._check_packed(ok, (2, 3, 64), 4, dev)
+    gptq._check_packed(torch.zeros(2, 3, 16, dtype=torch.int32), (2, 3, 64), 8, dev)
+    bad = [torch.zeros(2, 3, 9, dtype=torch.int32),            # wrong width
+           torch.zeros(2, 3, 8, dtype=torch.int64),            # wrong dtype
+           torch.zeros(2, 3, 16, dtype=torch.int32)[..., ::2]]  # not contiguous
+    for b in bad:
+        with pytest.raises(ValueError, match="packed_out"):
+            gptq._check_packed(b, (2, 3, 64), 4, dev)
+    with pytest.raises(ValueError, match="cannot pack"):
+        gptq._check_packed(ok, (2, 3, 64), 3, dev)
+    with pytest.raises(ValueError, match="packed_out"):
+        gptq._check_packed(ok, (2, 3, 64), 4, torch.device("meta"))
