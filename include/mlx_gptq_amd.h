@@ -256,6 +256,15 @@ int mgq_gptq_mxfp_solve_packed(const void* W, int w_dtype, int64_t B, int64_t R,
                                float* W_dq, float* rel_err, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* gptq.py:300-302 rel_err of an affine (or any) solve: rel[b] =
+ * ||W_dq[b] - W[b]||_F / max(||W[b]||_F, 1e-12), W_dq f32 [B, n], W [B, n] of
+ * w_dtype (f32 / bf16 / f16, read as it is), both contiguous. partials:
+ * double [B, n_partials, 2] scratch (1 <= n_partials <= 65535; each partial
+ * sums about n / n_partials elements in double, in a fixed order, so rel is
+ * deterministic); B <= 65535. */
+int mgq_rel_err(const float* W_dq, const void* W, int w_dtype, int64_t B, int64_t n,
+                double* partials, int64_t n_partials, float* rel, void* stream);
+
 /* Allocation-free variant of mgq_gptq_mxfp. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -730,6 +730,46 @@ __global__ void rel_err_kernel(const double* __restrict__ part, int64_t n_per_b,
   }
 }
 
+// Partial sums of gptq.py:300-302's rel_err for the affine path: block
+// (c, b) adds (W_dq - W)^2 and W^2 (in double) over elements
+// [c * chunk, (c + 1) * chunk) of item b, reduced in a fixed order, into
+// part[(b * nb + c) * 2 + {0, 1}] for rel_err_kernel. W is f32, bf16 or f16.
+template <typename TIn, bool IS_F16>
+__global__ void __launch_bounds__(256) rel_part_kernel(const float* __restrict__ W_dq,
+                                                       const TIn* __restrict__ W, int64_t n,
+                                                       int64_t chunk, double* __restrict__ part) {
+  const int64_t b = blockIdx.y, c = blockIdx.x;
+  const int64_t lo = c * chunk, hi = (lo + chunk < n) ? lo + chunk : n;
+  const float* dq = W_dq + b * n;
+  const TIn* w = W + b * n;
+  double num = 0.0, den = 0.0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    float x;
+    if constexpr (sizeof(TIn) == 4)
+      x = w[i];
+    else
+      x = IS_F16 ? f16_to_f32(w[i]) : bf16_to_f32(w[i]);
+    const float d = dq[i] - x;
+    num += static_cast<double>(d) * d;
+    den += static_cast<double>(x) * x;
+  }
+  __shared__ double sn[256], sd[256];
+  sn[threadIdx.x] = num;
+  sd[threadIdx.x] = den;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st) {
+      sn[threadIdx.x] += sn[threadIdx.x + st];
+      sd[threadIdx.x] += sd[threadIdx.x + st];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    part[(b * gridDim.x + c) * 2] = sn[0];
+    part[(b * gridDim.x + c) * 2 + 1] = sd[0];
+  }
+}
+
 struct WsLayout {
   int64_t dead_off, u_off, hc_off, rel_off, total;
 };
@@ -898,6 +938,35 @@ extern "C" int mgq_gptq_mxfp_solve_packed(const void* W, int w_dtype, int64_t B,
   MGQ_REQUIRE(packed_out != nullptr, MGQ_ERR_VALUE, "packed_out required");
   return solve_entry(W, w_dtype, B, R, C, mode, algorithm, offsets, n_offsets, q_out, packed_out,
                      scales_out, W_dq, rel_err, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mgq_rel_err(const float* W_dq, const void* W, int w_dtype, int64_t B, int64_t n,
+                           double* partials, int64_t n_partials, float* rel, void* stream) {
+  clear_error();
+  MGQ_REQUIRE(w_dtype == kF32 || w_dtype == kBF16 || w_dtype == kF16, MGQ_ERR_VALUE,
+              "unsupported weight dtype code %d", w_dtype);
+  MGQ_REQUIRE(B >= 0 && n >= 0, MGQ_ERR_SHAPE, "bad shape");
+  MGQ_REQUIRE(n_partials >= 1 && n_partials <= 65535, MGQ_ERR_VALUE,
+              "n_partials %lld outside 1..65535", (long long)n_partials);
+  if (B == 0) return MGQ_OK;
+  MGQ_REQUIRE(B <= 65535, MGQ_ERR_SHAPE, "rel_err: batch %lld exceeds 65535", (long long)B);
+  MGQ_REQUIRE(W_dq != nullptr && W != nullptr && partials != nullptr && rel != nullptr,
+              MGQ_ERR_VALUE, "rel_err: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t chunk = (n + n_partials - 1) / n_partials;
+  const dim3 grid(static_cast<unsigned>(n_partials), static_cast<unsigned>(B));
+  if (w_dtype == kF32)
+    rel_part_kernel<float, false><<<grid, 256, 0, st>>>(W_dq, static_cast<const float*>(W), n,
+                                                        chunk, partials);
+  else if (w_dtype == kBF16)
+    rel_part_kernel<uint16_t, false><<<grid, 256, 0, st>>>(
+        W_dq, static_cast<const uint16_t*>(W), n, chunk, partials);
+  else
+    rel_part_kernel<uint16_t, true><<<grid, 256, 0, st>>>(
+        W_dq, static_cast<const uint16_t*>(W), n, chunk, partials);
+  if (int rc = check_launch("rel_err partials")) return rc;
+  rel_err_kernel<<<static_cast<unsigned>(B), 256, 0, st>>>(partials, n_partials, B, rel);
+  return check_launch("rel_err");
 }
 
 extern "C" int mgq_gptq_mxfp(const void* W, int w_dtype, int64_t B, int64_t R, int64_t C,

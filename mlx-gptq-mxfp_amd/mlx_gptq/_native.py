@@ -76,6 +76,7 @@ SIGNATURES: dict[str, list] = {
     "mgq_gptq_mxfp_prepare": [_VP, _I64, _I64, _I64, _F32, _INT, _VP, _VP, _I64, _VP],
     "mgq_gptq_mxfp_solve": [_VP, _INT, _I64, _I64, _I64, _INT, _INT, _VP, _INT, _VP, _VP, _VP,
                             _VP, _VP, _I64, _VP],
+    "mgq_rel_err": [_VP, _VP, _INT, _I64, _I64, _VP, _I64, _VP, _VP],
     "mgq_gptq_mxfp_solve_packed": [_VP, _INT, _I64, _I64, _I64, _INT, _INT, _VP, _INT, _VP, _VP,
                                    _VP, _VP, _VP, _VP, _I64, _VP],
     "mgq_hinv_full_workspace_size": [_I64, _I64],

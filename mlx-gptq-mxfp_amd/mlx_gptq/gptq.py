@@ -317,11 +317,11 @@ def solve_gptq(
     # kept from before, and the retry's copy of W gets those columns zeroed
     # as the reference's dead-column fix does (gptq.py:216-222).
     dead = torch.diagonal(H_d, dim1=-2, dim2=-1) <= 0
-    W = W0.float().clone()
+    W = W0.to(torch.float32, copy=True)
     res = gptq_affine.gptq_quantize_affine(W, H_d, bits, group_size, damp, clip, storage_dtype,
                                            128, speculative=True)
     if res is None:
-        W = W0.float().clone()
+        W = W0.to(torch.float32, copy=True)
         W.masked_fill_(dead.unsqueeze(1), 0.0)
         res = gptq_quantize(W, H_d, bits, group_size, damp=damp, clip=clip,
                             storage_dtype=storage_dtype, mode=mode, mxfp_algorithm=mxfp_algorithm)

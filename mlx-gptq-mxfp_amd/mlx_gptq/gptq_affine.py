@@ -21,11 +21,30 @@ from .grid import _clip_code, _storage_code
 
 
 def rel_err(W_dq: torch.Tensor, W_orig: torch.Tensor) -> torch.Tensor:
-    """||W_dq - W_orig||_F / max(||W_orig||_F, 1e-12) per batch item (gptq.py:300-302)."""
-    W0 = W_orig.to(W_dq.device).float()
-    num = (W_dq - W0).pow(2).sum(dim=(1, 2)).sqrt()
-    den = W0.pow(2).sum(dim=(1, 2)).sqrt().clamp(min=1e-12)
-    return num / den
+    """||W_dq - W_orig||_F / max(||W_orig||_F, 1e-12) per batch item (gptq.py:300-302).
+
+    W_dq: f32 [B, ...] on a HIP device; W_orig the weights as given (f32, bf16
+    or f16 are read as they are, other dtypes as float32). One partial-sum
+    launch and one reduction (mgq_rel_err), sums in double."""
+    dev = W_dq.device
+    W0 = W_orig.to(dev)
+    if W0.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        W0 = W0.float()
+    W0 = W0.contiguous()
+    Wq = W_dq.contiguous()
+    B = int(Wq.shape[0])
+    n = int(Wq[0].numel()) if B else 0
+    rel = torch.empty(B, dtype=torch.float32, device=dev)
+    if B == 0:
+        return rel
+    nb = max(1, min(65535, -(-n // 4096)))  # about 4 K elements per partial
+    part = torch.empty(B, nb, 2, dtype=torch.float64, device=dev)
+    stream = nat.stream_of(dev)
+    for b0 in range(0, B, 65535):  # the partial launch's grid height
+        b1 = min(B, b0 + 65535)
+        nat.call("mgq_rel_err", Wq[b0].data_ptr(), W0[b0].data_ptr(), nat.dtype_code(W0.dtype),
+                 b1 - b0, n, part[b0].data_ptr(), nb, rel[b0:].data_ptr(), stream)
+    return rel
 
 
 def prepare_hinv_full(H: torch.Tensor, damp: float, max_attempts: int):

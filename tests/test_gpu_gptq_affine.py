@@ -399,3 +399,23 @@ def test_affine_shape_errors():
         gptq.gptq_quantize(W, H.clone(), 4, 64)
     with pytest.raises(AssertionError):
         gptq.gptq_quantize(W, torch.eye(64, device=DEV).unsqueeze(0), 4, 32)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+def test_rel_err_kernel_matches_the_reference_formula(dt):
+    """gptq_affine.rel_err (mgq_rel_err: double partial sums, fixed order)
+    against gptq.py:300-302's formula evaluated in float64 on the host; an
+    all-zero original takes the 1e-12 floor of the denominator; B = 3,
+    ragged n."""
+    from mlx_gptq import gptq_affine
+
+    g = torch.Generator().manual_seed(31)
+    W = (torch.randn(3, 37, 1001, generator=g) * 0.02).to(dt)
+    W[2] = 0
+    Wdq = W.float() + torch.randn(3, 37, 1001, generator=g) * 1e-3
+    got = gptq_affine.rel_err(Wdq.to(DEV), W.to(DEV)).cpu()
+    W64, D64 = W.double(), Wdq.double()
+    want = (D64 - W64).flatten(1).norm(dim=1) / W64.flatten(1).norm(dim=1).clamp(min=1e-12)
+    assert got.dtype == torch.float32
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=0)
+    assert want[2] > 1e10  # the floor case
