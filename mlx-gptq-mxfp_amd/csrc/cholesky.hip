@@ -50,10 +50,15 @@ __device__ inline double wave_sum_f64(double v) {
 
 // attempts[g*B + b]: 1..max_attempts on success, 0 if every attempt failed.
 // Hc (optional): compact [B*G][32][32] copy of each undamped block.
+// dead (optional): the dead-column fix of gptq.py:216-222 on the block's own
+// diagonal first -- an entry <= 0 marks its column dead (dead[b*C + c] = 1)
+// and becomes 1 in H, in place -- so the block is factored (and copied to
+// Hc) as the reference factors it after the fix. Without dead, H is only
+// read.
 __global__ void __launch_bounds__(64 * kWaves)
-    hinv32_kernel(const float* __restrict__ H, int64_t B, int64_t C, float damp,
-                  int max_attempts, float* __restrict__ U, int32_t* __restrict__ attempts,
-                  float* __restrict__ Hc) {
+    hinv32_kernel(float* H, int64_t B, int64_t C, float damp, int max_attempts,
+                  float* __restrict__ U, int32_t* __restrict__ attempts, float* __restrict__ Hc,
+                  uint8_t* __restrict__ dead) {
   __shared__ __attribute__((aligned(16))) double bcast[kWaves][kN];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -67,12 +72,28 @@ __global__ void __launch_bounds__(64 * kWaves)
   // the lane's 4x4 tile of the undamped block (rows 4p+r, columns 4q+c)
   float h[4][4];
   {
-    const float* src = H + b * C * C + (g * kN + 4 * p) * C + g * kN + 4 * q;
+    float* src = H + b * C * C + (g * kN + 4 * p) * C + g * kN + 4 * q;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float4 v = *reinterpret_cast<const float4*>(src + r * C);
       h[r][0] = v.x, h[r][1] = v.y, h[r][2] = v.z, h[r][3] = v.w;
-      if (Hc) *reinterpret_cast<float4*>(Hc + blk * kN * kN + (4 * p + r) * kN + 4 * q) = v;
+    }
+    if (dead != nullptr && p == q) {  // this lane holds diagonal entries 4p..4p+3
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool is_dead = h[r][r] <= 0.0f;
+        if (is_dead) {
+          h[r][r] = 1.0f;
+          src[r * C + r] = 1.0f;
+        }
+        dead[b * C + g * kN + 4 * p + r] = is_dead ? 1 : 0;
+      }
+    }
+    if (Hc) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float4*>(Hc + blk * kN * kN + (4 * p + r) * kN + 4 * q) =
+            float4{h[r][0], h[r][1], h[r][2], h[r][3]};
     }
   }
   // diag mean (fp64 sum, rounded once) clamped like torch .clamp(min=1e-8)
@@ -166,13 +187,14 @@ __global__ void __launch_bounds__(64 * kWaves)
 
 }  // namespace
 
-// Launch helper shared with the MXFP solver.
-int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, float* Hc, hipStream_t s) {
+// Launch helper shared with the MXFP solver (which passes dead, and so has
+// H's dead diagonals fixed in place by this launch).
+int launch_hinv32(float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
+                  int32_t* attempts, float* Hc, uint8_t* dead, hipStream_t s) {
   const int64_t n = B * (C / kN);
   if (n == 0) return MGQ_OK;
   hinv32_kernel<<<static_cast<unsigned>((n + kWaves - 1) / kWaves), 64 * kWaves, 0, s>>>(
-      H, B, C, damp, max_attempts, U, attempts, Hc);
+      H, B, C, damp, max_attempts, U, attempts, Hc, dead);
   return check_launch("hinv32");
 }
 
@@ -190,5 +212,7 @@ extern "C" int mgq_prepare_hinv_blocks(const float* H, int64_t B, int64_t C, int
   MGQ_REQUIRE(max_attempts >= 1, MGQ_ERR_VALUE, "max_attempts must be >= 1");
   MGQ_REQUIRE((reinterpret_cast<uintptr_t>(H) & 15u) == 0 && (reinterpret_cast<uintptr_t>(U) & 15u) == 0,
               MGQ_ERR_SHAPE, "H and U must be 16-byte aligned");
-  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, nullptr, as_stream(stream));
+  // without dead the kernel only reads H
+  return launch_hinv32(const_cast<float*>(H), B, C, damp, max_attempts, U, attempts, nullptr,
+                       nullptr, as_stream(stream));
 }

@@ -34,8 +34,8 @@
 
 namespace mgq {
 
-int launch_hinv32(const float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
-                  int32_t* attempts, float* Hc, hipStream_t s);
+int launch_hinv32(float* H, int64_t B, int64_t C, float damp, int max_attempts, float* U,
+                  int32_t* attempts, float* Hc, uint8_t* dead, hipStream_t s);
 
 namespace {
 
@@ -48,21 +48,6 @@ struct Offsets {
   int n;
   int v[kMaxOffsets];
 };
-
-// gptq.py:216-222: diag(H) <= 0 marks a dead column; its diagonal becomes 1
-// (in place) and its weights are treated as 0.
-__global__ void dead_fix_kernel(float* __restrict__ H, int64_t B, int64_t C,
-                                uint8_t* __restrict__ dead) {
-  const int64_t n = B * C;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = i / C, c = i % C;
-    float* d = H + b * C * C + c * C + c;
-    const bool is_dead = *d <= 0.0f;
-    if (is_dead) *d = 1.0f;
-    dead[i] = is_dead ? 1 : 0;
-  }
-}
 
 // Exact reference projection of one element (code and dq), w / scale done
 // as w * inv_scale (identical for power-of-two scales), on the hardware MX
@@ -836,9 +821,10 @@ extern "C" int mgq_gptq_mxfp_prepare(float* H, int64_t B, int64_t R, int64_t C, 
   uint8_t* dead = reinterpret_cast<uint8_t*>(ws + L.dead_off);
   float* U = reinterpret_cast<float*>(ws + L.u_off);
   float* Hcmp = reinterpret_cast<float*>(ws + L.hc_off);
-  dead_fix_kernel<<<elementwise_blocks(B * C, 256), 256, 0, st>>>(H, B, C, dead);
-  if (int rc = check_launch("dead-column fix")) return rc;
-  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, st);
+  // the dead-column fix (gptq.py:216-222: diag(H) <= 0 marks a dead column,
+  // its diagonal becomes 1 in place, its weights are treated as 0) runs in
+  // the same launch, each 32x32 block fixing its own diagonal first
+  return launch_hinv32(H, B, C, damp, max_attempts, U, attempts, Hcmp, dead, st);
 }
 
 namespace mgq {
