@@ -251,3 +251,11 @@ def test_moe_config4_full_size():
     for codes in (q, qd, *rtn):
         words = packing.pack_q(codes, 4).cpu().view(torch.int32).numpy().view(np.uint32)
         assert np.array_equal(words, packing_ref.pack_q(codes.cpu().numpy(), 4))
+    # the bench's path: the solver packing its own codes gives the same codes
+    # and pack_q's words for the whole gate_up layer (no routed expert has a
+    # dead column, so the first solve's in-place fix left Hg as it was)
+    assert bool((Hg[:ne].diagonal(dim1=1, dim2=2) > 0).all())
+    packed = torch.empty(ne, q.shape[1], q.shape[2] // 8, dtype=torch.int32, device=DEV)
+    q2, s2, _, W_dq2, _ = gptq.solve_gptq(L.W_gate_up[:ne], Hg[:ne], **kw, packed_out=packed)
+    assert torch.equal(q2, q) and torch.equal(s2, s) and torch.equal(W_dq2, W_dq)
+    assert torch.equal(packed, packing.pack_q(q, 4).view(torch.int32))
