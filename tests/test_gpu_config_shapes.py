@@ -81,14 +81,15 @@ def _scale_gate(kw: dict) -> float:
     """Scale-byte agreement required: groupwise scales are choose_mxfp_scale
     of the original weights (gptq.py:102-106), deterministic, so every byte
     must match; the safe search's argmin over candidate objectives can flip
-    at near-ties."""
+    at near-ties (none did on 130,944 config-4 scale bytes, 31 experts x 48
+    rows of both projections), so at most one byte in a thousand may."""
     alg = kw.get("mxfp_algorithm", "auto")
     if alg == "auto":
         alg = "safe-scale-search" if kw.get("mode") == "mxfp4" else "groupwise"
-    return 1.0 if alg == "groupwise" else 0.99
+    return 1.0 if alg == "groupwise" else 0.999
 
 
-def _check(agree, s_agree, pl, pl_ref, s_gate=0.99):
+def _check(agree, s_agree, pl, pl_ref, s_gate=0.999):
     assert agree >= 0.995, agree
     assert s_agree >= s_gate, s_agree
     assert torch.all((pl - pl_ref).abs() <= 0.01 * pl_ref.abs()), (pl, pl_ref)
