@@ -78,6 +78,11 @@ def test_affine_matches_reference_golden(name):
     _check_vs(W, q, s, b, W_dq, t[f"{name}.q"], t[f"{name}.scales"], t[f"{name}.biases"],
               t[f"{name}.W_dq"], t[f"{name}.H_after"])
     assert torch.allclose(rel.cpu(), t[f"{name}.rel"], rtol=5e-3)
+    # observed: every code equal to the reference's, and every rounded
+    # (bf16 / f16) scale and bias; held to that
+    assert torch.equal(q.cpu(), t[f"{name}.q"])
+    if s.dtype != torch.float32:
+        assert torch.equal(s.cpu(), t[f"{name}.scales"]) and torch.equal(b.cpu(), t[f"{name}.biases"])
 
 
 @pytest.mark.parametrize("bits,G,clip,storage,block", [

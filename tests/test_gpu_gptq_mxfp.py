@@ -58,6 +58,9 @@ def test_mxfp_matches_reference_golden(name):
     assert _agree(q, t[f"{name}.q"]) >= 0.995
     # groupwise scales are choose_mxfp_scale of the weights: deterministic
     assert _agree(s, t[f"{name}.scales"]) >= (1.0 if kw["mxfp_algorithm"] == "groupwise" else 0.99)
+    # observed: every code and scale byte of every golden case equal to the
+    # reference's; held to that, so a change that moves one shows up here
+    assert torch.equal(q.cpu(), t[f"{name}.q"]) and torch.equal(s.cpu(), t[f"{name}.scales"])
     # W_dq is exactly the decode of (q, scales)
     assert torch.equal(grid.dequantize_artifact(q, s, None, kw["mode"], 32), W_dq)
     Href = t[f"{name}.H_after"]
