@@ -15,8 +15,10 @@
 //      quadratic form err^T Hg err, strict '<' so the first best wins;
 //   2. 32-step GPTQ with the chosen fixed scale:
 //        dq_c = Q(w_c);  err = (w_c - dq_c) / U[c,c];  w_j -= err * U[c,j] (j>c)
-//      (sub and IEEE div as torch does them; the update w_j -= err * U[c,j]
-//      as one fused multiply-add, where torch rounds the product first);
+//      computed as a_c = w_c - dq_c and w_j -= a_c * V[c,j] with
+//      V[c,j] = U[c,j] / U[c,c] formed once per block, one fused
+//      multiply-add per update (torch rounds err, the product and the
+//      difference; the two agree to an ulp or two per term);
 //   3. safe search keeps the GPTQ result only if its objective <= the best
 //      RTN candidate's;
 //   4. range guard: every |dq| <= max(32 * max|orig|, 2^-126), else the RTN
@@ -118,22 +120,35 @@ struct HSplit {
   u32x4_t v[3][2][kG][2];
 };
 
-__device__ inline void split3(float x, __bf16& a, __bf16& b, __bf16& c) {
-  a = static_cast<__bf16>(x);
-  const float r = x - static_cast<float>(a);  // exact
-  b = static_cast<__bf16>(r);
-  c = static_cast<__bf16>(r - static_cast<float>(b));  // exact, and exact in bf16
+// Two values rounded to bf16 as one packed word (v_cvt_pk_bf16_f32), and the
+// halves of such a word widened back to fp32.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2v_t));
 }
+__device__ inline float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
+// The three-way split of eight values: x = a + b + c with a = RN_bf16(x),
+// b = RN_bf16(x - a), c = x - a - b (each difference exact, and c exact in
+// bf16), two values at a time: each part is rounded as a pair and widened
+// back from the packed word.
 __device__ inline void split3x8(const float* x, bf16x8_t& a, bf16x8_t& b, bf16x8_t& c) {
+  u32x4_t pa, pb, pc;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    __bf16 p, q, r;
-    split3(x[j], p, q, r);
-    a[j] = p;
-    b[j] = q;
-    c[j] = r;
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t wa = pk_bf16(x[2 * p], x[2 * p + 1]);
+    const float r0 = x[2 * p] - bf16_lo(wa), r1 = x[2 * p + 1] - bf16_hi(wa);  // exact
+    const uint32_t wb = pk_bf16(r0, r1);
+    const float s0 = r0 - bf16_lo(wb), s1 = r1 - bf16_hi(wb);  // exact, and exact in bf16
+    pa[p] = wa;
+    pb[p] = wb;
+    pc[p] = pk_bf16(s0, s1);
   }
+  a = __builtin_bit_cast(bf16x8_t, pa);
+  b = __builtin_bit_cast(bf16x8_t, pb);
+  c = __builtin_bit_cast(bf16x8_t, pc);
 }
 
 // Fill the workgroup's HSplit from the compact Hessian block (row-major
@@ -303,9 +318,12 @@ __device__ inline float mx4_encode_into(uint32_t& word, int k, float w, float in
 
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 
-// The 32 weights of one (row, group), 16-byte loads, widened to fp32.
+// The 32 weights of one (row, group), 16-byte loads, widened to fp32; for
+// 16-bit weights also the loaded words (weights 2k, 2k+1 in word k).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 template <typename TIn, bool IS_F16>
-__device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float (&v)[kG]) {
+__device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float (&v)[kG],
+                                  uint32_t (&raw)[kG / 2]) {
   if constexpr (sizeof(TIn) == 4) {
     const float4* p = reinterpret_cast<const float4*>(W + base);
 #pragma unroll
@@ -324,6 +342,7 @@ __device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float
       const uint32_t d[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        raw[4 * i + k] = d[k];
         const uint16_t lo = static_cast<uint16_t>(d[k] & 0xffffu);
         const uint16_t hi = static_cast<uint16_t>(d[k] >> 16);
         v[8 * i + 2 * k] = IS_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
@@ -366,12 +385,12 @@ __global__ void __launch_bounds__(kThreads)
   // compact (post dead-column fix) Hessian block, written by hinv32
   const float* __restrict__ Hg = Hc + (b * G + g) * kG * kG;
   const int lane = threadIdx.x & 63;
-  // U^T staged in LDS (Ut[c][k] = U[k][c]): the recurrence below reads one
-  // column of U per step with broadcast LDS loads (uniform addresses).
+  // V^T staged in LDS (Ut[c][k] = V[k][c] = U[k][c] / U[k][k], k < c): the
+  // recurrence below reads one column of V per step with broadcast LDS loads
+  // (uniform addresses).
   __shared__ float Ut[kG * kG];
-  // RN(1/U[c][c]) for the correctly rounded divisions of the recurrence
+  // RN(1/U[k][k]), or 0 where U[k][k] is outside [2^-24, 2^24]
   __shared__ float ydiag[kG];
-  __shared__ int ydiag_zero_s;
   // the safe search's objective operand: Hg as three exact bf16 parts
   HSplit* hs = nullptr;
   if constexpr (SAFE) {
@@ -380,19 +399,34 @@ __global__ void __launch_bounds__(kThreads)
   }
   {
     const float* Ub = U + (b * G + g) * kG * kG;
-    for (int e = threadIdx.x; e < kG * kG; e += kThreads) Ut[(e % kG) * kG + e / kG] = Ub[e];
-    // wave 0 also records whether any reciprocal is 0 (a divisor outside
-    // [2^-24, 2^24]), for the whole workgroup
-    const float yv = threadIdx.x < kG ? div_exact_recip(Ub[threadIdx.x * (kG + 1)]) : 1.0f;
-    if (threadIdx.x < kG) ydiag[threadIdx.x] = yv;
-    if (threadIdx.x < 64) {
-      const bool z = __builtin_amdgcn_ballot_w64(!(yv != 0.0f)) != 0;
-      if (threadIdx.x == 0) ydiag_zero_s = z ? 1 : 0;
-    }
+    if (threadIdx.x < kG) ydiag[threadIdx.x] = div_exact_recip(Ub[threadIdx.x * (kG + 1)]);
     if constexpr (SAFE) stage_hsplit(Hg, hs);
+    __syncthreads();
+    // V = U[k][c] * RN(1/U[k][k]); a divisor outside [2^-24, 2^24] divides
+    constexpr int kPer = kG * kG / kThreads;
+    float u[kPer], y[kPer];
+    bool any_div = false;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) u[i] = Ub[threadIdx.x + i * kThreads];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      y[i] = ydiag[(threadIdx.x + i * kThreads) / kG];
+      any_div |= y[i] == 0.0f;
+    }
+    if (any_div) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int k = (threadIdx.x + i * kThreads) / kG;
+        if (y[i] == 0.0f) u[i] = u[i] / Ub[k * (kG + 1)];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = threadIdx.x + i * kThreads;
+      Ut[(e % kG) * kG + e / kG] = y[i] == 0.0f ? u[i] : u[i] * y[i];
+    }
   }
   __syncthreads();
-  const bool ydiag_zero = ydiag_zero_s != 0;
   const uint8_t* __restrict__ dd = dead + b * C + g * kG;
   const int64_t base = (b * R + r) * C + g * kG;
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
@@ -409,15 +443,25 @@ __global__ void __launch_bounds__(kThreads)
   float den = 0.0f, dead_sq = 0.0f;
   {
     float v[kG];
-    load_group<TIn, IS_F16>(W, base, v);
+    uint32_t raw[kG / 2];
+    load_group<TIn, IS_F16>(W, base, v, raw);
     // dead columns (gptq.py:219-221) read as 0
     const uint4 m0 = reinterpret_cast<const uint4*>(dd)[0];
     const uint4 m1 = reinterpret_cast<const uint4*>(dd)[1];
     const uint32_t mw[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
     const bool any_dead = (m0.x | m0.y | m0.z | m0.w | m1.x | m1.y | m1.z | m1.w) != 0u;  // uniform
     if (rel_part) {
+      if constexpr (sizeof(TIn) == 2 && !IS_F16) {
+        // bf16 pairs: both exact products and their sum in one instruction
 #pragma unroll
-      for (int i = 0; i < kG; ++i) den = fmaf(v[i], v[i], den);
+        for (int k = 0; k < kG / 2; ++k) {
+          const bf16x2_t x = __builtin_bit_cast(bf16x2_t, raw[k]);
+          den = __builtin_amdgcn_fdot2_f32_bf16(x, x, den, false);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kG; ++i) den = fmaf(v[i], v[i], den);
+      }
       if (any_dead) {
 #pragma unroll
         for (int i = 0; i < kG; ++i)
@@ -431,14 +475,12 @@ __global__ void __launch_bounds__(kThreads)
     }
     // amax = max |v|, NaN when any v is NaN (grid.py's amax propagates it;
     // which NaN does not matter: e8m0_exponent and the range guard only
-    // test for one). Magnitudes order like their bit patterns, NaN above
-    // infinity, so an unsigned max of the patterns gives exactly that.
-    {
-      uint32_t mb = 0u;
+    // test for one): IEEE maximum propagates NaN, three operands at a time.
+    amax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kG; ++i) mb = max(mb, f2u(v[i]) & 0x7fffffffu);
-      amax = __uint_as_float(mb);
-    }
+    for (int i = 0; i < kG; i += 2)
+      amax = __builtin_elementwise_maximum(
+          amax, __builtin_elementwise_maximum(fabsf(v[i]), fabsf(v[i + 1])));
 #pragma unroll
     for (int p = 0; p < kG / 2; ++p)
       *reinterpret_cast<float2*>(so + p * 2 * kThreads + 2 * threadIdx.x) = make_float2(v[2 * p], v[2 * p + 1]);
@@ -514,32 +556,25 @@ __global__ void __launch_bounds__(kThreads)
 
   // 2. GPTQ recurrence with the fixed scale, column by column. The
   // reference updates all later columns after each step
-  // (W[c+1:] -= err_c * U[c, c+1:]); each element therefore sees
-  // w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) - ... in that order.
-  // Forming w_c lazily from the stored errors keeps that order while keeping
-  // only err[] live. Each step is one fused multiply-add (the reference
-  // rounds err_k U[k,c] before subtracting it): half the instructions of the
-  // two-op form, and the codes it gives agree with the reference's on
-  // practically every element (none differed on a 12.6 M-code sample of the
-  // config-4 layer).
+  // (W[c+1:] -= err_c * U[c, c+1:], err_c = (w_c - dq_c) / U[c,c]); each
+  // element therefore sees w_c = ((orig_c - err_0 U[0,c]) - err_1 U[1,c]) -
+  // ... in that order. Forming w_c lazily keeps that order while keeping
+  // only one value per column live: the numerator a_k = w_k - dq_k, with the
+  // division moved onto the factor, err_k U[k,c] = a_k V[k,c] (V staged
+  // above, each entry rounded once). Each step is one fused multiply-add,
+  // where the reference rounds err_k, then err_k U[k,c], then the
+  // difference: the terms agree to an ulp or two, and so do the codes on
+  // practically every element.
   //
-  // The divisions take Markstein's correction without a branch (EXACT =
-  // false; a zero numerator may come out as a zero of either sign, which no
-  // output can see: errors only feed the later columns' sums, and a zero sum
-  // of either sign encodes to code 0 and decodes to +0) and only record the
-  // numerators' range: their smallest nonzero magnitude (as a bit pattern
-  // shifted left by one, minus 2, so that a zero wraps to the top) and their
-  // largest. If one fell outside the correction's exact range, or a NaN
-  // appeared (it reaches the last error through every later column), the
-  // wave runs the recurrence again with div_exact (EXACT = true); a divisor
-  // outside [2^-24, 2^24] (ydiag 0) sends the workgroup there directly. The
-  // fast pass also encodes without the NaN patch (a NaN w_c reaches the last
-  // error as well, so its codes are never kept).
+  // The fast pass (EXACT = false) encodes without the NaN patch; a NaN w_c
+  // reaches the last numerator through every later column (NaN times V is
+  // NaN, zero entries included), which sends the wave to the exact pass. A
+  // zero numerator may come out as a zero of either sign, which no output
+  // can see: numerators only feed the later columns' sums, and a zero sum of
+  // either sign encodes to code 0 and decodes to +0.
   float errs[kG];
   auto recurrence = [&](auto exact_tag) __attribute__((always_inline)) -> bool {
     constexpr bool EXACT = decltype(exact_tag)::value;
-    uint32_t mag_lo = 0xffffffffu;
-    float mag_hi = 0.0f;
 #pragma unroll
     for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
     // Ut's base, passed from column to column through lds_after so that its
@@ -548,7 +583,7 @@ __global__ void __launch_bounds__(kThreads)
     const lds_f32* ubase = (const lds_f32*)Ut;
 #pragma unroll
     for (int c = 0; c < kG; ++c) {
-      // column c of U (row c of Ut, 16-byte aligned), read 4 values at a time
+      // column c of V (row c of Ut, 16-byte aligned), read 4 values at a time
       if (c) ubase = lds_after(ubase, errs[c - 1]);
       const lds_f32* col = ubase + c * kG;
       float acc = ORIG(c);
@@ -564,22 +599,13 @@ __global__ void __launch_bounds__(kThreads)
         dq = mx4_encode_into(codes[c / 4], c % 4, acc, inv_scale, scale);
       else
         code = quant_exact<MODE, !EXACT>(acc, inv_scale, scale, &dq);
-      const float a = acc - dq;  // errs[c] = a / U[c][c]
-      if constexpr (EXACT) {
-        errs[c] = div_exact(a, col[c], ydiag[c]);
-      } else {
-        const float y = ydiag[c], q = a * y;
-        errs[c] = fmaf(fmaf(-q, col[c], a), y, q);
-        mag_lo = min(mag_lo, (f2u(a) << 1) - 2u);
-        mag_hi = fmaxf(mag_hi, fabsf(a));
-      }
+      errs[c] = acc - dq;
       if constexpr (!(MODE == kMxfp4 && !EXACT)) codes[c / 4] |= code << (8 * (c % 4));
       dq_set(c, dq);
     }
-    return (mag_lo < (27u << 24) - 2u) | !(mag_hi < 0x1p101f) |
-           (errs[kG - 1] != errs[kG - 1]);
+    return errs[kG - 1] != errs[kG - 1];
   };
-  if (ydiag_zero || __builtin_amdgcn_ballot_w64(recurrence(std::false_type{})) != 0)
+  if (__builtin_amdgcn_ballot_w64(recurrence(std::false_type{})) != 0)
     recurrence(std::true_type{});
 
   // The GPTQ result's dequantized values, decoded once for the objective
@@ -609,14 +635,24 @@ __global__ void __launch_bounds__(kThreads)
     for (int i = 0; i < kG; ++i) ok = ok & (fabsf(w[i]) <= limit);  // no short-circuit branches
   }
   if (!ok) {  // RTN baseline at the chosen scale
+    // A NaN weight is the only input that the NaN-free encode gets wrong (its
+    // n = w * inv_scale is NaN exactly when w is), and amax is NaN exactly
+    // when a weight is: without one among this wave's fallback lanes, MXFP4
+    // takes the encode that writes each code straight into its byte.
+    if (MODE == kMxfp4 && __builtin_amdgcn_ballot_w64(amax != amax) == 0) {
 #pragma unroll
-    for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
+      for (int i = 0; i < kG; ++i)
+        w[i] = mx4_encode_into(codes[i / 4], i % 4, ORIG(i), inv_scale, scale);
+    } else {
 #pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      float dq;
-      const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
-      codes[i / 4] |= code << (8 * (i % 4));
-      w[i] = dq;
+      for (int i = 0; i < kG / 4; ++i) codes[i] = 0u;
+#pragma unroll
+      for (int i = 0; i < kG; ++i) {
+        float dq;
+        const uint32_t code = quant_exact<MODE>(ORIG(i), inv_scale, scale, &dq);
+        codes[i / 4] |= code << (8 * (i % 4));
+        w[i] = dq;
+      }
     }
   }
 

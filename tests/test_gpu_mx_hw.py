@@ -45,7 +45,8 @@ def test_hw_mx_conversions_exhaustive(e):
 
 
 def test_markstein_division_matches_ieee():
-    """div_exact (the recurrence's err = (w - dq) / U[c,c], gptq.py:160-170)
+    """div_exact, the correction and range guards that the affine column
+    loop's divisions take (err = (w - q) / U[c,c] and the clip scale),
     against IEEE fp32 division, bit for bit: every 64th divisor significand
     against all 2^23 dividend significands (the full 2^46 pairs were checked
     the same way with stride 1), plus random pairs over the exponent range
