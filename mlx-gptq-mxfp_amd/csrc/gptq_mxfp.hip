@@ -42,7 +42,12 @@ int launch_hinv32(float* H, int64_t B, int64_t C, float damp, int max_attempts, 
 namespace {
 
 constexpr int kG = 32;
-constexpr int kThreads = 256;
+// 512 threads (8 waves) per workgroup: the per-workgroup LDS (the weights'
+// 64 KB plus Ut, the H split and ydiag, 74 KB in all) lets two workgroups
+// share a CU, i.e. 4 waves per SIMD, which the kernel reaches in 128 VGPRs
+// without spilling (amdgpu_waves_per_eu below). With 256 threads the fixed
+// part would hold the CU to 3 workgroups, 3 waves per SIMD.
+constexpr int kThreads = 512;
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dealt round-robin
 constexpr int kMaxOffsets = 8;
 
@@ -226,6 +231,8 @@ __device__ inline float mfma_objective(const float (&e)[kG], const HSplit* hs, i
     MGQ_MFMA2(h1, x3, y3);
     MGQ_MFMA2(h2, x2, y2);
     MGQ_MFMA2(h3, x1, y1);
+    // one K-chunk's split operands live at a time
+    __builtin_amdgcn_sched_barrier(0);
   }
   return objective_from(e, d0, d1);
 }
@@ -355,7 +362,7 @@ __device__ inline void load_group(const TIn* __restrict__ W, int64_t base, float
 // XERR: the candidate errors are exact in bf16 (bf16 weights, offsets within
 // the bound the host checks), so their objective uses mfma_objective_x1.
 template <typename TIn, bool IS_F16, int MODE, bool SAFE, bool XERR>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
     mxfp_solve_kernel(const TIn* __restrict__ W, int64_t B, int64_t R, int64_t C,
                       const float* __restrict__ Hc, const float* __restrict__ U,
                       const uint8_t* __restrict__ dead,
@@ -432,7 +439,7 @@ __global__ void __launch_bounds__(kThreads)
   const float fmax = (MODE == kMxfp4) ? 6.0f : 448.0f;
 
   // The group's 32 (dead-column-fixed) weights live in LDS as fp32, not in
-  // registers, which leaves room for 3 waves per SIMD without spills.
+  // registers, which leaves room for 4 waves per SIMD without spills.
   // Weights 2p and 2p+1 of thread t sit side by side at
   // so[p * 2 kThreads + 2t], so a pair is one 8-byte read and both pair and
   // single reads are conflict-free.
@@ -608,32 +615,40 @@ __global__ void __launch_bounds__(kThreads)
   if (__builtin_amdgcn_ballot_w64(recurrence(std::false_type{})) != 0)
     recurrence(std::true_type{});
 
-  // The GPTQ result's dequantized values, decoded once for the objective
-  // below, the range guard and the stores.
-  float w[kG];
-#pragma unroll
-  for (int i = 0; i < kG; ++i) w[i] = DQ(i);
-  // 3. GPTQ vs best RTN candidate (safe search only)
-  bool use_gptq = true;
-  if (SAFE) {
-    float err[kG];
-#pragma unroll
-    for (int i0 = 0; i0 < kG; i0 += 8) {
-#pragma unroll
-      for (int i = i0; i < i0 + 8; ++i) err[i] = (w[i] - ORIG(i)) * inv_scale;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    use_gptq = __builtin_amdgcn_ldexpf(mfma_objective(err, hs, lane), 2 * (e_sel - e0)) <= best;
-  }
-  // 4. range guard on the selected result
+  // 4's test first: the range guard on the GPTQ result, every |dq| <= limit;
+  // and (safe search) the result's errors for step 3, from the same decode.
+  // The dequantized values are not kept through the objective (they are
+  // decoded again below), which keeps the objective's registers in budget.
   float limit = amax * 32.0f;
   const float floor_ = __uint_as_float(0x00800000u);  // 2^-126
   limit = (limit != limit) ? limit : fmaxf(limit, floor_);
-  bool ok = use_gptq;
-  if (use_gptq) {
+  bool in_range = true;
+  float err[SAFE ? kG : 1];
 #pragma unroll
-    for (int i = 0; i < kG; ++i) ok = ok & (fabsf(w[i]) <= limit);  // no short-circuit branches
+  for (int i0 = 0; i0 < kG; i0 += 8) {
+#pragma unroll
+    for (int i = i0; i < i0 + 8; ++i) {
+      const float wi = DQ(i);
+      in_range = in_range & (fabsf(wi) <= limit);  // no short-circuit branches
+      if constexpr (SAFE) err[i] = (wi - ORIG(i)) * inv_scale;
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // 3. GPTQ vs best RTN candidate (safe search only)
+  bool use_gptq = true;
+  if constexpr (SAFE)
+    use_gptq = __builtin_amdgcn_ldexpf(mfma_objective(err, hs, lane), 2 * (e_sel - e0)) <= best;
+  const bool ok = use_gptq & in_range;
+  if constexpr (SAFE) {
+    // opaque to the compiler, so that the values are decoded again here
+    // rather than kept from the loop above
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kG / 4; ++i) asm volatile("" : "+v"(codes[i]));
+  }
+  float w[kG];
+#pragma unroll
+  for (int i = 0; i < kG; ++i) w[i] = DQ(i);
   if (!ok) {  // RTN baseline at the chosen scale
     // A NaN weight is the only input that the NaN-free encode gets wrong (its
     // n = w * inv_scale is NaN exactly when w is), and amax is NaN exactly
