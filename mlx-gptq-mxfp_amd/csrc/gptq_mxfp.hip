@@ -307,21 +307,6 @@ __device__ inline float decode_code(uint32_t word, int k, float scale) {
   }
 }
 
-// The recurrence's fast-pass MXFP4 encode (mx4_encode_hw_nonan) of one
-// column, written straight into byte k of its codes word: the conversion
-// stores the code and a zero code in that byte and keeps the other three,
-// so no shift and merge is needed; dq is decoded from the same byte.
-__device__ inline float mx4_encode_into(uint32_t& word, int k, float w, float inv_scale,
-                                        float scale) {
-  const float n = w * inv_scale + 0.0f;  // -0 -> +0, as mx4_encode_hw_nonan
-  switch (k) {
-    case 0: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 0); break;
-    case 1: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 1); break;
-    case 2: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 2); break;
-    default: word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 3); break;
-  }
-  return decode_code<kMxfp4>(word, k, scale);
-}
 
 __device__ inline float nan_max(float m, float a) { return (a > m || a != a) ? a : m; }
 

@@ -110,6 +110,30 @@ __device__ inline uint32_t mx4_encode_hw_nonan(float w, float inv_scale, float s
   return code;
 }
 
+// mx4_encode_hw_nonan written straight into byte k of `word` (one code per
+// byte): the conversion stores the code and a zero code in that byte and
+// keeps the other three, so no shift and merge is needed; dq is decoded from
+// the same byte with the scale passed in. k must be a compile-time constant
+// once the caller unrolls (the byte select is an immediate).
+__device__ inline float mx4_encode_into(uint32_t& word, int k, float w, float inv_scale,
+                                        float scale) {
+  const float n = w * inv_scale + 0.0f;  // -0 -> +0, as mx4_encode_hw_nonan
+  switch (k) {
+    case 0:
+      word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 0);
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 0)[0];
+    case 1:
+      word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 1);
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 1)[0];
+    case 2:
+      word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 2);
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 2)[0];
+    default:
+      word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, n, 0.0f, 1.0f, 3);
+      return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, scale, 3)[0];
+  }
+}
+
 // Exact E4M3 code of clamp(n, +-448) and dq = value(code) * scale
 // (= e4m3_code_clamped(clamp448(n)), e4m3_value(code) * scale).
 __device__ inline uint32_t mx8_encode_hw(float w, float inv_scale, float scale, float* dq) {

@@ -16,6 +16,11 @@
 //      2^-126 <= |n| < 512
 //   7  MXFP8 error not exact in bf16 although w is a bf16 value and
 //      2^-126 <= |n| < 16384
+//   8  mx4_encode_into (the NaN-free encode written into one byte of a
+//      word) != mx4_encode in code or dq bits, or a neighbouring byte
+//      changed, for every w whose n is not NaN
+//   9  mx8_encode_hw_nonan != mx8_encode_hw in code or dq bits, for every w
+//      whose n is not NaN
 //
 // mgq_hwcheck_scaled_decode(counts): the scaled decodes with the scale
 // folded in against the decode at scale 1 times the scale, bit for bit
@@ -39,7 +44,7 @@ using namespace mgq;
 
 namespace {
 
-constexpr int kKinds = 8;
+constexpr int kKinds = 10;
 
 __device__ inline bool same_bits(float a, float b) { return f2u(a) == f2u(b) || (a != a && b != b); }
 __device__ inline bool tiny(float x) { return !(fabsf(x) >= 1.17549435e-38f) && x == x; }
@@ -88,6 +93,20 @@ __global__ void check_kernel(int e, unsigned long long* counts) {
       const bool w_bf16 = bf16_exact(w[j]);
       loc[6] += (w_bf16 && !small && an < 512.0f && !bf16_exact(e4[j]));
       loc[7] += (w_bf16 && !small && an < 16384.0f && !bf16_exact(e8[j]));
+      if (n == n) {
+        // byte j % 4 of a word whose other bytes hold a marker
+        const int k = j & 3;
+        uint32_t word = 0xa5a5a5a5u;
+        const float dq_in = mx4_encode_into(word, k, w[j], inv, scale);
+        const uint32_t byte = (word >> (8 * k)) & 0xffu;
+        const uint32_t rest = word | (0xffu << (8 * k));
+        loc[8] += (byte != c_ref) || !same_bits(dq_in, dq_ref) ||
+                  rest != (0xa5a5a5a5u | (0xffu << (8 * k)));
+        float dq8_nn, dq8;
+        const uint32_t k_nn = mx8_encode_hw_nonan(w[j], inv, scale, &dq8_nn);
+        const uint32_t k_ex = mx8_encode_hw(w[j], inv, scale, &dq8);
+        loc[9] += (k_nn != k_ex) || !same_bits(dq8_nn, dq8);
+      }
     }
   }
 #pragma unroll
@@ -164,7 +183,7 @@ __global__ void scaled_decode_kernel(unsigned long long* counts) {
   if (bad8) atomicAdd(&counts[1], bad8);
 }
 
-// Runs the MX check for scale exponent e in [-127, 127]; counts: host array of 8.
+// Runs the MX check for scale exponent e in [-127, 127]; counts: host array of 10.
 extern "C" int mgq_hwcheck_mx(int e, unsigned long long* counts) {
   if (e < -127 || e > 127) return -1;
   unsigned long long* d = nullptr;

@@ -5,7 +5,9 @@ csrc/mgq_common.h (themselves pinned to the reference's threshold chain,
 grid.py:82-105, by tests/test_mx4_projection.py, and to torch's float8_e4m3fn
 cast by the encoder tests):
 
-- codes and dq of the recurrence's encoders: bit-exact;
+- codes and dq of the recurrence's encoders: bit-exact; the NaN-free forms
+  (the fast pass and the RTN fallback) bit-exact for every non-NaN n, the
+  MXFP4 one as written into one byte of a codes word;
 - candidate errors (q - n) used to score scale candidates: bit-exact except
   where n = w / scale is below 2^-126 in magnitude, where both are below it;
 - for bf16 weights those errors are exact in bf16 whenever
@@ -26,7 +28,7 @@ pytestmark = pytest.mark.gpu
 
 LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "libmgq_hwcheck.so")
 KINDS = ["mx4 code", "mx4 dq", "mx8 code", "mx8 dq", "mx4 cand err", "mx8 cand err",
-         "mx4 err not bf16", "mx8 err not bf16"]
+         "mx4 err not bf16", "mx8 err not bf16", "mx4 NaN-free byte encode", "mx8 NaN-free encode"]
 
 
 @pytest.mark.parametrize("e", [-127, -126, -125, -64, -9, -1, 0, 1, 7, 64, 119, 120, 126, 127])
@@ -38,7 +40,7 @@ def test_hw_mx_conversions_exhaustive(e):
         pytest.fail(f"{LIB} missing: run build() first")
     lib = ctypes.CDLL(LIB)
     lib.mgq_hwcheck_mx.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_ulonglong)]
-    counts = (ctypes.c_ulonglong * 8)()
+    counts = (ctypes.c_ulonglong * len(KINDS))()
     assert lib.mgq_hwcheck_mx(e, counts) == 0
     bad = {k: int(c) for k, c in zip(KINDS, counts) if c}
     assert not bad, (e, bad)
