@@ -609,15 +609,26 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
   limit = (limit != limit) ? limit : fmaxf(limit, floor_);
   bool in_range = true;
   float err[SAFE ? kG : 1];
+  if constexpr (SAFE) {
+    // in units of the scale: the decode at scale 1 is dq / 2^e exactly, so
+    // |dq| <= limit is |value| <= limit * 2^-e (exact: the product stays
+    // normal or becomes inf for every reachable (amax, e)), and
+    // err = (dq - w) * 2^-e = value - w * 2^-e, one fused multiply-add with
+    // the same rounding as the difference scaled afterwards
+    const float limit_u = limit * inv_scale;
 #pragma unroll
-  for (int i0 = 0; i0 < kG; i0 += 8) {
+    for (int i0 = 0; i0 < kG; i0 += 8) {
 #pragma unroll
-    for (int i = i0; i < i0 + 8; ++i) {
-      const float wi = DQ(i);
-      in_range = in_range & (fabsf(wi) <= limit);  // no short-circuit branches
-      if constexpr (SAFE) err[i] = (wi - ORIG(i)) * inv_scale;
+      for (int i = i0; i < i0 + 8; ++i) {
+        const float v = decode_code<MODE>(codes[i / 4], i % 4, 1.0f);
+        in_range = in_range & (fabsf(v) <= limit_u);  // no short-circuit branches
+        err[i] = fmaf(ORIG(i), -inv_scale, v);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kG; ++i) in_range = in_range & (fabsf(DQ(i)) <= limit);
   }
   // 3. GPTQ vs best RTN candidate (safe search only)
   bool use_gptq = true;
