@@ -4,10 +4,12 @@
 //
 // Every 32-column group of every row is independent: it sees only its own
 // 32x32 Hessian block Hg and the block's upper Cholesky-inverse factor U
-// (hinv32). One thread owns one (batch item, row, group): its 32 weights stay
-// in registers through the whole recurrence, so nothing touches HBM between
-// reading W and writing (q, W_dq, scale byte). All lanes of a workgroup share
-// (b, g), so Hg and U are wave-uniform and are read with scalar loads.
+// (hinv32). One thread owns one (batch item, row, group): its 32 weights sit
+// in LDS and its codes and errors in registers through the whole solve, so
+// nothing touches HBM between reading W and writing (q, packed q, W_dq,
+// scale byte). All lanes of a workgroup share (b, g): Hg (as bf16 parts)
+// and U (as V, each row scaled by its diagonal's reciprocal) are staged once
+// per workgroup in LDS and read there with uniform addresses.
 //
 // Per (row, group), in the reference's order:
 //   1. scale choice: groupwise = round(log2(max|w|/fmax)) (E8M0); safe =
@@ -16,7 +18,7 @@
 //   2. 32-step GPTQ with the chosen fixed scale:
 //        dq_c = Q(w_c);  err = (w_c - dq_c) / U[c,c];  w_j -= err * U[c,j] (j>c)
 //      computed as a_c = w_c - dq_c and w_j -= a_c * V[c,j] with
-//      V[c,j] = U[c,j] / U[c,c] formed once per block, one fused
+//      V[c,j] = U[c,j] * RN(1/U[c,c]) formed once per block, one fused
 //      multiply-add per update (torch rounds err, the product and the
 //      difference; the two agree to an ulp or two per term);
 //   3. safe search keeps the GPTQ result only if its objective <= the best
@@ -264,7 +266,7 @@ __device__ inline float mfma_objective_x1(const float (&e)[kG], const HSplit* hs
 // An opaque zero that depends on `v`: addresses built from it cannot be
 // computed before `v`, so the loads behind them are neither hoisted out of
 // the loop nor scheduled far ahead of their use (without this the compiler
-// lifts the U block out of the recurrence and runs out of registers).
+// lifts the V block out of the recurrence and runs out of registers).
 __device__ inline int zero_after(float v) {
   int z;
   asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(v));
