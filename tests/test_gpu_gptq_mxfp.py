@@ -91,6 +91,33 @@ def test_mxfp_matches_oracle_larger(mode, alg):
     assert torch.all((pl - pl_ref).abs() <= 0.01 * pl_ref.abs()), (pl, pl_ref)
 
 
+@pytest.mark.parametrize("h_scale", [1e18, 1e24])
+def test_extreme_hessian_scales_vs_oracle(h_scale):
+    """H scaled so far that every diagonal of the factor U lies below 2^-24
+    (U[c,c] ~ 1 / sqrt(H[c,c])): the solver then forms V = U[c,j] / U[c,c]
+    by IEEE division instead of the reciprocal product. (Above 2^24 is out
+    of reach: the damping's floor, 0.01 * max(mean diag, 1e-8), keeps
+    U[c,c] <= 1e5.) GPTQ is invariant to the scale of H (the damping is
+    relative to its mean diagonal), so the codes must still follow the
+    oracle's on the same scaled H, and the unscaled solve's; every diagonal
+    really is below the range (checked here)."""
+    from mlx_gptq import gptq
+
+    W, H, _ = _setup(B=2, R=128, C=128, N=1024, seed=21, scale=0.02)
+    H = H * h_scale
+    U = gptq_ref.prepare_hinv(H.clone(), 0.01)
+    d = torch.diagonal(U, dim1=-2, dim2=-1).abs()
+    assert bool((d < 2.0 ** -24).all())
+    Wb = W.to(torch.bfloat16)
+    q, s, _, W_dq, _ = gptq.solve_gptq(Wb.to(DEV), H.clone().to(DEV), 4, 32, mode="mxfp4")
+    rq, rs, _, rW, _ = gptq_ref.solve_gptq(Wb, H.clone(), 4, 32, mode="mxfp4")
+    assert _agree(q, rq) >= 0.995
+    assert _agree(s, rs) >= 0.99
+    assert torch.isfinite(W_dq.cpu()).all()
+    q1, s1, _, _, _ = gptq.solve_gptq(Wb.to(DEV), (H / h_scale).to(DEV), 4, 32, mode="mxfp4")
+    assert _agree(q, q1) >= 0.995
+
+
 @pytest.mark.parametrize("mode,alg", [("mxfp4", "safe-scale-search"), ("mxfp4", "groupwise"),
                                       ("mxfp8", "groupwise")])
 def test_negative_zero_weights_encode_as_the_reference(mode, alg):
