@@ -379,9 +379,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
   // compact (post dead-column fix) Hessian block, written by hinv32
   const float* __restrict__ Hg = Hc + (b * G + g) * kG * kG;
   const int lane = threadIdx.x & 63;
-  // V^T staged in LDS (Ut[c][k] = V[k][c] = U[k][c] / U[k][k], k < c): the
-  // recurrence below reads one column of V per step with broadcast LDS loads
-  // (uniform addresses).
+  // V^T staged in LDS (Ut[c][k] = V[k][c] = U[k][c] * RN(1/U[k][k]); the
+  // recurrence reads the entries k < c): one column of V per step with
+  // broadcast LDS loads (uniform addresses).
   __shared__ float Ut[kG * kG];
   // RN(1/U[k][k]), or 0 where U[k][k] is outside [2^-24, 2^24]
   __shared__ float ydiag[kG];
